@@ -1,0 +1,76 @@
+"""The C-ABI library: it loads, exports every entry point include/triton_mla.h
+declares, and rejects bad arguments before touching a device (no GPU needed)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "triton_mla.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tmla_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from triton_mla import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.fail(f"HIP library not built: {_native.LIB_PATH} (run __graft_entry__.build())")
+    return _native.load()
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    assert {"tmla_mla_decode", "tmla_mla_decode_partial", "tmla_mla_decode_combine",
+            "tmla_workspace_bytes", "tmla_last_error", "tmla_version", "tmla_device_cu_count"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from triton_mla import _native
+
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in triton_mla.h but not exported"
+        assert name in _native.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_workspace_arithmetic(lib):
+    # uniform: batch * splits slots; balanced: workers + batch slots (float32 partial + lse)
+    def expect(slots, heads, dv=512):
+        o = slots * heads * dv * 4
+        return ((o + 255) // 256) * 256 + slots * heads * 4
+
+    assert lib.tmla_workspace_bytes(32, 128, 512, 8, 0) == expect(256, 128)
+    assert lib.tmla_workspace_bytes(32, 128, 512, 0, 256) == expect(288, 128)
+    assert lib.tmla_workspace_bytes(3, 20, 512, 1, 0) == expect(3, 20)
+    assert lib.tmla_version() >= 100
+
+
+def _partial(lib, **kw):
+    args = dict(q=None, qsb=576 * 128, qsh=576, kv=None, kv0=64 * 576, kv1=576, nblocks=4, page=64,
+                bt=None, btsb=1, btcols=1, seqlens=None, batch=2, heads=128, dv=512, dr=64, dtype=0,
+                scale=0.1, splits=1, workers=0, out=None, osb=128 * 512, osh=512, lse=None, ws=None,
+                wsb=0, stream=None)
+    args.update(kw)
+    return lib.tmla_mla_decode_partial(*args.values())
+
+
+def test_invalid_arguments_rejected_on_host(lib):
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    ws = lib.tmla_workspace_bytes(2, 128, 512, 1, 0)
+    assert _partial(lib, dtype=7, ws=fake, wsb=ws) == 1
+    assert b"dtype" in lib.tmla_last_error()
+    assert _partial(lib, dv=256, ws=fake, wsb=ws) == 2  # unsupported head_dim_v
+    assert _partial(lib, ws=None, wsb=0) == 3  # workspace missing
+    assert _partial(lib, ws=fake, wsb=ws - 1) == 3  # workspace too small
+    assert _partial(lib, splits=0, workers=0, ws=fake, wsb=ws) == 1  # balanced needs workers
+    assert _partial(lib, heads=0, ws=fake, wsb=ws) == 1
+    # null tensors are caught before any launch
+    assert _partial(lib, ws=fake, wsb=ws) == 1
+    assert b"null" in lib.tmla_last_error()

@@ -1,0 +1,784 @@
+// MLA decode attention for MI355X (gfx950): split-KV partial kernel, log-sum-exp
+// combine kernel and the C ABI declared in include/triton_mla.h.
+//
+// Reference behaviour: src/triton_mla/kernel.py (stage 1 kernel.py:43-138,
+// stage 2 kernel.py:141-181, host wrapper kernel.py:204-323).
+//
+// Design (one workgroup = one worker, 64 * NW threads, NW waves of 32 heads):
+//  * Each worker owns a range of 64-token tiles; it walks them as 32-token
+//    sub-tiles through a 4-stage LDS ring. Rows are copied HBM -> LDS with
+//    global_load_lds_dwordx4 (no VGPR staging): one instruction moves eight
+//    full 128-byte lines (8 token rows x 128 bytes) into 1 KiB of LDS.
+//  * Each LDS sub-tile is used twice: as K (all 576 dims) for
+//    S^T = K . Q^T and as V (first 512 dims) for O^T += V^T . P^T, both on
+//    v_mfma_f32_32x32x16_{bf16,f16}. V^T operands come straight from the
+//    row-major tile through ds_read_b64_tr_b16.
+//  * Q stays in VGPRs for the whole range (32 heads x 576 dims per wave);
+//    O^T (32 heads x 512 dims, fp32) lives in accumulation registers.
+//  * Online softmax in the base-2 domain with a lazy rescale: the running
+//    reference max only moves when a new score exceeds it by more than 2^8,
+//    so probabilities stay <= 256 and the O^T rescale is rare.
+//  * The combine kernel merges per-sequence partials exactly like the
+//    reference's stage 2.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "triton_mla.h"
+
+namespace tmla {
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define LDS_AS __attribute__((address_space(3)))
+
+constexpr int kTileTokens = 64;     // planning unit (one page at page_size 64)
+constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
+constexpr int kStages = 4;          // LDS ring depth (3 sub-tiles in flight)
+constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
+constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (p <= 2^8)
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct PartialArgs {
+  const char* q;           // element pointer (bytes)
+  int64_t q_sb, q_sh;      // element strides
+  const char* kv;
+  int64_t kv_s0, kv_s1;    // byte strides: block (dense: batch), token
+  int64_t num_blocks;
+  int32_t page_size, page_shift;  // page_shift = log2(page_size) or -1
+  const int32_t* bt;
+  int64_t bt_sb;
+  int32_t bt_cols;
+  const int32_t* seqlens;
+  int32_t batch, num_heads;
+  float qk_scale_log2;
+  int32_t num_splits, num_workers;
+  char* out;
+  int64_t out_sb, out_sh;  // element strides
+  float* lse;
+  float* mid_o;            // [slots, H, DV]
+  float* mid_lse;          // [slots, H], base-2
+};
+
+struct CombineArgs {
+  const int32_t* seqlens;
+  int32_t batch, num_heads;
+  int32_t num_splits, num_workers;
+  char* out;
+  int64_t out_sb, out_sh;
+  float* lse;
+  const float* mid_o;
+  const float* mid_lse;
+};
+
+// ---------------------------------------------------------------------------
+// small device helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int tiles_of(int n) { return n > 0 ? (n + kTileTokens - 1) / kTileTokens : 0; }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// Register-class pins: an empty asm that requires its operand in VGPRs /
+// AGPRs at that point. They keep the PV accumulators in AGPRs and the S tile
+// in VGPRs instead of letting the allocator shuttle blocks between files.
+__device__ __forceinline__ void pin_vgpr(f32x16& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x)); }
+
+// Workgroup barrier that the compiler treats as a full memory-ordering point
+// but that adds no counter waits of its own: the producer side waits for its
+// LDS-DMA copies with wait_vmcnt first.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int DT>
+struct Elt;
+template <>
+struct Elt<TMLA_BF16> {
+  __device__ static __forceinline__ f32x16 mfma(i16x8 a, i16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ short from_float(float x) {
+    return __builtin_bit_cast(short, (__bf16)x);
+  }
+};
+template <>
+struct Elt<TMLA_FP16> {
+  __device__ static __forceinline__ f32x16 mfma(i16x8 a, i16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ short from_float(float x) {
+    return __builtin_bit_cast(short, (_Float16)x);
+  }
+};
+
+// XOR swizzle of the 16-byte piece index inside an 8-row x 128-byte LDS
+// block. Row r of row-group rg: keeps the S^T operand reads (16 lanes = 16
+// rows, one piece) and the V^T transpose reads (32 lanes = 4 rows x 4 pieces)
+// on distinct banks.
+__device__ __forceinline__ int piece_swizzle(int r, int rg) {
+  return (((r >> 1) & 1) << 2) | ((r >> 2) & 1) | ((rg & 1) << 1);
+}
+
+// Byte offset of the row of (local) token `tok` of sequence b inside kv.
+// Token indices past the sequence end are clamped to its last token so every
+// copied row is real cache memory (its scores are masked to -inf later).
+template <bool PAGED>
+__device__ __forceinline__ int64_t row_offset(const PartialArgs& a, int b, int tok, int n_b,
+                                              int page_id) {
+  const int t = min(tok, n_b - 1);
+  // dense caches hold num_blocks (= capacity) rows per sequence
+  if (!PAGED) return (int64_t)b * a.kv_s0 + (int64_t)min(t, (int)(a.num_blocks - 1)) * a.kv_s1;
+  const int in_page = a.page_shift >= 0 ? (t & (a.page_size - 1)) : (t % a.page_size);
+  return (int64_t)page_id * a.kv_s0 + (int64_t)in_page * a.kv_s1;
+}
+
+__device__ __forceinline__ int page_slot_of(const PartialArgs& a, int t) {
+  const int s = a.page_shift >= 0 ? (t >> a.page_shift) : (t / a.page_size);
+  return min(s, a.bt_cols - 1);
+}
+
+__device__ __forceinline__ int load_page(const PartialArgs& a, int b, int slot) {
+  int p = a.bt[(int64_t)b * a.bt_sb + slot];
+  p = p < 0 ? 0 : p;
+  return (int64_t)p >= a.num_blocks ? (int)(a.num_blocks - 1) : p;
+}
+
+// Segment of a worker: tiles [t0, t1) of sequence b, result goes to `slot`
+// (a partial) or straight to out/lse when `direct`.
+struct Segment {
+  int b, t0, t1, slot;
+  bool direct;
+};
+
+// ---------------------------------------------------------------------------
+// Stage 1: split-KV partial attention
+// ---------------------------------------------------------------------------
+//
+// LDS stage (one 32-token sub-tile): 4 row-groups x NCB column blocks of 1 KiB;
+// block (rg, cb) holds rows 8rg..8rg+7, bytes [128cb, 128cb+128) of each row,
+// 16-byte piece p of row r at position r*8 + (p ^ piece_swizzle(r, rg)).
+template <int DT, int DV, int DR, int NW, bool PAGED, bool PAGE_UNIFORM>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(1, 1)))
+void mla_partial_kernel(PartialArgs a) {
+  constexpr int DQK = DV + DR;
+  static_assert(DQK % 64 == 0 && DV % 64 == 0, "row must be whole 128-byte blocks");
+  constexpr int NCB = DQK / 64;           // 128-byte column blocks per row
+  constexpr int NKC = DQK / 16;           // k-chunks of QK^T
+  constexpr int NDB = DV / 32;            // 32-dim blocks of PV
+  constexpr int BLOCKS = 4 * NCB;         // 1 KiB blocks per stage
+  constexpr int STAGE = BLOCKS * 1024;
+  constexpr int RG_PER_WAVE = 4 / NW;
+  constexpr int LOADS = RG_PER_WAVE * NCB;  // DMA instructions per wave per sub-tile
+  static_assert(NW == 1 || NW == 2 || NW == 4, "waves per workgroup");
+  static_assert(LOADS < 64, "vmcnt immediate range");
+  // vmcnt is a 6-bit counter: with more than 63 copies outstanding behind the
+  // sub-tile we wait for, wait for a later point instead (over-waiting is safe)
+  constexpr int WAIT2 = 2 * LOADS < 64 ? 2 * LOADS : LOADS;
+
+  __shared__ __attribute__((aligned(1024))) char smem[kStages * STAGE];
+  __shared__ int s_scan[256];
+  __shared__ int s_info[4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int worker = blockIdx.x;
+  const int head_base = blockIdx.y * (kHeadsPerWave * NW) + wave * kHeadsPerWave;
+  const int head = head_base + (lane & 31);
+  const bool head_ok = head < a.num_heads;
+  const int hi = lane >> 5;  // which half of the 32-token M block / k slots
+
+  // ---- work range -------------------------------------------------------
+  int b_first, tile_lo, tile_hi, off_first, chunk = 0;
+  if (a.num_splits > 0) {
+    const int S = a.num_splits;
+    const int b = worker / S, s = worker - b * S;
+    const int nt = tiles_of(a.seqlens[b]);
+    const int spt = (nt + S - 1) / S;
+    tile_lo = s * spt;
+    tile_hi = min(tile_lo + spt, nt);
+    b_first = b;
+    off_first = 0;
+  } else {
+    // Balanced: the T tiles of all sequences (in order) are cut into
+    // num_workers ranges of c = cdiv(T, num_workers) tiles.
+    const int nthreads = 64 * NW;
+    const int per = (a.batch + nthreads - 1) / nthreads;
+    const int lo_b = min(tid * per, a.batch), hi_b = min(lo_b + per, a.batch);
+    int sum = 0;
+    for (int b = lo_b; b < hi_b; ++b) sum += tiles_of(a.seqlens[b]);
+    s_scan[tid] = sum;
+    __syncthreads();
+    // inclusive scan over the per-thread chunk sums (Hillis-Steele in LDS)
+    for (int d = 1; d < nthreads; d <<= 1) {
+      const int v = tid >= d ? s_scan[tid - d] : 0;
+      __syncthreads();
+      s_scan[tid] += v;
+      __syncthreads();
+    }
+    const int total = __builtin_amdgcn_readfirstlane(s_scan[nthreads - 1]);
+    chunk = (total + a.num_workers - 1) / a.num_workers;
+    const int lo = worker * chunk;
+    if (tid == 0) s_info[0] = -1;
+    __syncthreads();
+    if (lo < total) {
+      int off = s_scan[tid] - sum;  // exclusive prefix of this thread's chunk
+      if (off <= lo && lo < off + sum) {
+        for (int b = lo_b; b < hi_b; ++b) {
+          const int nt = tiles_of(a.seqlens[b]);
+          if (lo < off + nt) {
+            s_info[0] = b;
+            s_info[1] = off;
+            break;
+          }
+          off += nt;
+        }
+      }
+    }
+    __syncthreads();
+    if (s_info[0] < 0) return;
+    b_first = __builtin_amdgcn_readfirstlane(s_info[0]);
+    off_first = __builtin_amdgcn_readfirstlane(s_info[1]);
+    tile_lo = lo - off_first;  // local to b_first
+    tile_hi = min(lo + chunk, total) - off_first;  // may run past b_first
+  }
+  if (tile_lo >= tile_hi) return;
+
+  // per-lane LDS read offsets inside a stage
+  // S^T A operand: token = lane%32 (rg = (lane%32)/8, r = lane%8), piece = 2*(kc%4) + hi
+  int k_off[4];
+  {
+    const int rg = (lane & 31) >> 3, r = lane & 7;
+    const int sw = piece_swizzle(r, rg);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) k_off[j] = rg * NCB * 1024 + (r * 8 + ((2 * j + hi) ^ sw)) * 16;
+  }
+  // V^T operand via ds_read_b64_tr_b16: group g = lane/16, L = lane%16;
+  // read e2 covers tokens 16c + 8e2 + 4(g/2) + L/4, dims 32db + 16(g%2) + 4(L%4).
+  int v_off[2][2];  // [db&1][e2]
+  {
+    const int g = lane >> 4, L = lane & 15;
+    const int r = 4 * (g >> 1) + (L >> 2);
+#pragma unroll
+    for (int dbp = 0; dbp < 2; ++dbp)
+#pragma unroll
+      for (int e2 = 0; e2 < 2; ++e2) {
+        const int piece = 4 * dbp + 2 * (g & 1) + ((L & 3) >> 1);
+        v_off[dbp][e2] = e2 * NCB * 1024 + (r * 8 + (piece ^ piece_swizzle(r, e2))) * 16 + 8 * (L & 1);
+      }
+  }
+  // DMA: this lane copies, for each of its wave's row-groups, the piece
+  // (lane%8) ^ swizzle of token row 8rg + lane/8.
+  const int dma_r = lane >> 3;
+
+  // ---- segments -----------------------------------------------------------
+  int b = b_first;
+  int t_start = tile_lo;       // local tile index within b
+  int remaining = tile_hi - tile_lo;  // tiles left in this worker's range
+  int seg_global_off = off_first;     // balanced mode: tile offset of b
+
+  while (remaining > 0) {
+    const int n_b = a.seqlens[b];
+    const int nt_b = tiles_of(n_b);
+    if (nt_b == 0) {  // only possible in balanced mode between sequences
+      ++b;
+      continue;
+    }
+    const int t_end = min(nt_b, t_start + remaining);
+    Segment seg;
+    seg.b = b;
+    seg.t0 = t_start;
+    seg.t1 = t_end;
+    if (a.num_splits > 0) {
+      const int S = a.num_splits;
+      const int spt = (nt_b + S - 1) / S;
+      const int count = (nt_b + spt - 1) / spt;
+      seg.slot = b * S + t_start / spt;
+      seg.direct = count == 1;
+    } else {
+      const int g1 = seg_global_off / chunk, g2 = (seg_global_off + nt_b - 1) / chunk;
+      seg.slot = worker + b;
+      seg.direct = g1 == g2;
+    }
+
+    // ---- Q operands for this sequence -------------------------------------
+    i16x8 qop[NKC];
+    {
+      const short* qrow = reinterpret_cast<const short*>(a.q) + (int64_t)b * a.q_sb +
+                          (int64_t)(head_ok ? head : 0) * a.q_sh + 8 * hi;
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) {
+        i16x8 v = *reinterpret_cast<const i16x8*>(qrow + 16 * kc);
+        qop[kc] = head_ok ? v : (i16x8)0;
+      }
+    }
+
+    f32x16 acc[NDB];
+#pragma unroll
+    for (int d = 0; d < NDB; ++d) acc[d] = (f32x16)0.0f;
+    float m_run = -INFINITY;  // base-2 reference max (per head)
+    float l_run = 0.0f;       // sum of p over this lane's half of the tokens
+
+    // sub-tiles of 32 tokens; the last one may be partially valid and a
+    // trailing fully-invalid half tile is skipped
+    const int st0 = 2 * seg.t0;
+    const int st1 = min(2 * seg.t1, (n_b + kSubTokens - 1) / kSubTokens);
+    const int nst = st1 - st0;
+
+    auto issue = [&](int st) {
+      char LDS_AS* stage = (char LDS_AS*)(void LDS_AS*)smem + (st - st0) % kStages * STAGE;
+      const int tok_base = st * kSubTokens;
+      int page = 0;
+      if (PAGED && PAGE_UNIFORM) page = load_page(a, b, page_slot_of(a, tok_base));
+#pragma unroll
+      for (int i = 0; i < RG_PER_WAVE; ++i) {
+        const int rg = wave * RG_PER_WAVE + i;
+        const int tok = tok_base + rg * 8 + dma_r;
+        int pg = page;
+        if (PAGED && !PAGE_UNIFORM) pg = load_page(a, b, page_slot_of(a, min(tok, n_b - 1)));
+        const char* row = a.kv + row_offset<PAGED>(a, b, tok, n_b, pg);
+        const int piece = (lane & 7) ^ piece_swizzle(dma_r, rg);
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+          __builtin_amdgcn_global_load_lds(row + cb * 128 + piece * 16,
+                                           (void LDS_AS*)(stage + (rg * NCB + cb) * 1024), 16, 0, 0);
+        }
+      }
+    };
+
+    // prologue: up to kStages-1 sub-tiles in flight
+#pragma unroll
+    for (int i = 0; i < kStages - 1; ++i)
+      if (i < nst) issue(st0 + i);
+
+    for (int i = 0; i < nst; ++i) {
+      const int st = st0 + i;
+      // wait for this wave's copies of sub-tile st, then for everyone's
+      const int ahead = min(nst - 1 - i, kStages - 2);
+      if (PAGED && !PAGE_UNIFORM) {
+        wait_vmcnt<0>();
+      } else if (ahead >= 2) {
+        wait_vmcnt<WAIT2>();
+      } else if (ahead == 1) {
+        wait_vmcnt<LOADS>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      lds_barrier();
+      // the stage read in the previous iteration is free again
+      if (i + kStages - 1 < nst) issue(st + kStages - 1);
+
+      const char LDS_AS* stage = (const char LDS_AS*)(const void LDS_AS*)smem + i % kStages * STAGE;
+
+      // ---- S^T = K . Q^T over all DQK dims (32 tokens x 32 heads) --------
+      f32x16 s = (f32x16)0.0f;
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) {
+        const i16x8 kop =
+            *reinterpret_cast<const i16x8 LDS_AS*>(stage + k_off[kc & 3] + (kc >> 2) * 1024);
+        s = Elt<DT>::mfma(kop, qop[kc], s);
+      }
+      pin_vgpr(s);
+
+      // ---- online softmax (base 2) ----------------------------------------
+      const int tok0 = st * kSubTokens + 4 * hi;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tok = tok0 + 8 * (r >> 2) + (r & 3);
+        const float x = tok < n_b ? s[r] * a.qk_scale_log2 : -INFINITY;
+        s[r] = x;
+        mx = fmaxf(mx, x);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run, mx);
+      // lazy rescale: move the reference only when a score exceeds it by 2^8
+      const bool need = m_new > m_run + kRescaleLog2;
+      if (__builtin_amdgcn_ballot_w64(need)) {
+        if (m_run != -INFINITY) {
+          const float alpha = fast_exp2(m_run - m_new);
+          l_run *= alpha;
+          // one 16-register block at a time, so the accumulators stay in AGPRs
+#pragma unroll
+          for (int d = 0; d < NDB; ++d) {
+            f32x16 t = acc[d];
+            pin_vgpr(t);
+            t *= alpha;
+            acc[d] = t;
+            pin_agpr(acc[d]);
+          }
+        }
+        m_run = m_new;
+      }
+      i16x8 pop[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(s[r] - m_run);
+        l_run += p;
+        pop[r >> 3][r & 7] = Elt<DT>::from_float(p);
+      }
+
+      // ---- O^T += V^T . P^T  (512 dims x 32 heads, k = 32 tokens) --------
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const int base = c * 2 * NCB * 1024 + (db >> 1) * 1024;
+          const i16x4 lo = __builtin_bit_cast(
+              i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                         (i16x4 LDS_AS*)(stage + v_off[db & 1][0] + base)));
+          const i16x4 hi4 = __builtin_bit_cast(
+              i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                         (i16x4 LDS_AS*)(stage + v_off[db & 1][1] + base)));
+          const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+          acc[db] = Elt<DT>::mfma(vop, pop[c], acc[db]);
+          pin_agpr(acc[db]);
+        }
+      }
+    }
+    // all waves must be done with the ring before the next segment refills it
+    lds_barrier();
+
+    // ---- finalize: out = acc / l, lse2 = m + log2(l) -------------------------
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const bool has = l_tot > 0.0f;
+    const float inv = has ? 1.0f / l_tot : 0.0f;
+    const float lse2 = has ? m_run + fast_log2(l_tot) : -INFINITY;
+    if (head_ok) {
+      if (seg.direct) {
+        short* orow = reinterpret_cast<short*>(a.out) + (int64_t)b * a.out_sb + (int64_t)head * a.out_sh;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            i16x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = Elt<DT>::from_float(acc[db][4 * q4 + e] * inv);
+            *reinterpret_cast<i16x4*>(orow + 32 * db + 8 * q4 + 4 * hi) = v;
+          }
+        if (hi == 0) a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
+      } else {
+        float* orow = a.mid_o + ((int64_t)seg.slot * a.num_heads + head) * DV;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[db][4 * q4 + e] * inv;
+            *reinterpret_cast<f32x4*>(orow + 32 * db + 8 * q4 + 4 * hi) = v;
+          }
+        if (hi == 0) a.mid_lse[(int64_t)seg.slot * a.num_heads + head] = lse2;
+      }
+    }
+
+    remaining -= (t_end - t_start);
+    seg_global_off += nt_b;
+    ++b;
+    t_start = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Stage 2: log-sum-exp merge (kernel.py:159-181). One wave per (b, head).
+// ---------------------------------------------------------------------------
+template <int DT, int DV>
+__global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
+  static_assert(DV % 256 == 0, "8 dims per lane");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = blockIdx.x;
+  const int head = blockIdx.y * 4 + wave;
+  __shared__ int s_red[2][4];
+
+  // partial slots of sequence b
+  const int n_b = a.seqlens[b];
+  const int nt_b = tiles_of(n_b);
+  int slot0 = 0, count = 0;
+  if (a.num_splits > 0) {
+    const int S = a.num_splits;
+    if (nt_b > 0) {
+      const int spt = (nt_b + S - 1) / S;
+      count = (nt_b + spt - 1) / spt;
+    }
+    slot0 = b * S;
+  } else {
+    int before = 0, total = 0;
+    for (int i = threadIdx.x; i < a.batch; i += 256) {
+      const int nt = tiles_of(a.seqlens[i]);
+      total += nt;
+      if (i < b) before += nt;
+    }
+    for (int d = 32; d >= 1; d >>= 1) {
+      before += __shfl_xor(before, d);
+      total += __shfl_xor(total, d);
+    }
+    if (lane == 0) {
+      s_red[0][wave] = before;
+      s_red[1][wave] = total;
+    }
+    __syncthreads();
+    before = s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3];
+    total = s_red[1][0] + s_red[1][1] + s_red[1][2] + s_red[1][3];
+    if (nt_b > 0) {
+      const int chunk = (total + a.num_workers - 1) / a.num_workers;
+      const int g1 = before / chunk, g2 = (before + nt_b - 1) / chunk;
+      count = g2 - g1 + 1;
+      slot0 = g1 + b;
+    }
+  }
+  if (head >= a.num_heads || count == 1) return;  // count == 1: written by stage 1
+
+  short* orow = reinterpret_cast<short*>(a.out) + (int64_t)b * a.out_sb + (int64_t)head * a.out_sh;
+  if (count == 0) {  // empty sequence: out = 0, lse = -inf (kernel.py:126-128, 178-181)
+    for (int d = lane * 8; d < DV; d += 512) *reinterpret_cast<i16x8*>(orow + d) = (i16x8)0;
+    if (lane == 0) a.lse[(int64_t)b * a.num_heads + head] = -INFINITY;
+    return;
+  }
+  // m = max over splits of lse2 (-inf -> 0)
+  float m = -INFINITY;
+  for (int s = lane; s < count; s += 64)
+    m = fmaxf(m, a.mid_lse[(int64_t)(slot0 + s) * a.num_heads + head]);
+  for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+  if (m == -INFINITY) m = 0.0f;
+
+  for (int d0 = 0; d0 < DV; d0 += 512) {
+    f32x4 acc0 = (f32x4)0.0f, acc1 = (f32x4)0.0f;
+    float wsum = 0.0f;
+    for (int s = 0; s < count; ++s) {
+      const int64_t row = (int64_t)(slot0 + s) * a.num_heads + head;
+      const float w = fast_exp2(a.mid_lse[row] - m);
+      wsum += w;
+      if (w > 0.0f) {  // empty splits carry lse -inf and no partial data
+        const float* src = a.mid_o + row * DV + d0 + lane * 8;
+        acc0 += w * *reinterpret_cast<const f32x4*>(src);
+        acc1 += w * *reinterpret_cast<const f32x4*>(src + 4);
+      }
+    }
+    const float inv = wsum > 0.0f ? 1.0f / wsum : 1.0f;
+    i16x8 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = Elt<DT>::from_float(acc0[e] * inv);
+      v[4 + e] = Elt<DT>::from_float(acc1[e] * inv);
+    }
+    *reinterpret_cast<i16x8*>(orow + d0 + lane * 8) = v;
+    if (d0 == 0 && lane == 0)
+      a.lse[(int64_t)b * a.num_heads + head] = wsum > 0.0f ? (m + fast_log2(wsum)) * kLn2 : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+thread_local char g_err[512] = "no error";
+
+int fail(int code, const char* msg) {
+  snprintf(g_err, sizeof(g_err), "%s", msg);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  snprintf(g_err, sizeof(g_err), "%s: %s", where, hipGetErrorString(e));
+  return TMLA_ERR_HIP;
+}
+
+size_t workspace_bytes(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
+  if (batch < 0 || heads < 0 || dv < 0) return 0;
+  const int64_t slots = splits > 0 ? (int64_t)batch * splits : (int64_t)workers + batch;
+  const size_t o = (size_t)slots * heads * dv * sizeof(float);
+  const size_t l = (size_t)slots * heads * sizeof(float);
+  return ((o + 255) & ~(size_t)255) + l;
+}
+
+struct Common {
+  int32_t batch, heads, dv, dr, dtype, splits, workers;
+};
+
+int check_common(const Common& c, const void* workspace, size_t ws_bytes) {
+  if (c.batch < 0 || c.heads <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "batch must be >= 0 and num_heads > 0");
+  if (c.dtype != TMLA_BF16 && c.dtype != TMLA_FP16) return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16 or TMLA_FP16");
+  if (c.splits < 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "num_splits must be >= 0");
+  if (c.splits == 0 && c.workers <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "num_workers must be > 0 when num_splits == 0");
+  if (c.splits > 0 && (int64_t)c.batch * c.splits > INT32_MAX) return fail(TMLA_ERR_INVALID_ARGUMENT, "batch * num_splits overflows");
+  if (c.dv != 512) return fail(TMLA_ERR_UNSUPPORTED, "head_dim_v must be 512");
+  const size_t need = workspace_bytes(c.batch, c.heads, c.dv, c.splits, c.workers);
+  if (need > 0 && (workspace == nullptr || ws_bytes < need))
+    return fail(TMLA_ERR_WORKSPACE_TOO_SMALL, "workspace is missing or smaller than tmla_workspace_bytes()");
+  return TMLA_OK;
+}
+
+template <int DT, int NW, bool PAGED, bool UNI>
+hipError_t launch_partial_t(const PartialArgs& a, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((mla_partial_kernel<DT, 512, 64, NW, PAGED, UNI>), grid, dim3(64 * NW), 0, stream, a);
+  return hipGetLastError();
+}
+
+template <int DT, int NW>
+hipError_t launch_partial_nw(const PartialArgs& a, dim3 grid, hipStream_t stream, bool paged, bool uni) {
+  if (!paged) return launch_partial_t<DT, NW, false, false>(a, grid, stream);
+  if (uni) return launch_partial_t<DT, NW, true, true>(a, grid, stream);
+  return launch_partial_t<DT, NW, true, false>(a, grid, stream);
+}
+
+template <int DT>
+hipError_t launch_partial_dt(const PartialArgs& a, dim3 grid, int nw, hipStream_t stream, bool paged, bool uni) {
+  if (nw == 1) return launch_partial_nw<DT, 1>(a, grid, stream, paged, uni);
+  if (nw == 2) return launch_partial_nw<DT, 2>(a, grid, stream, paged, uni);
+  return launch_partial_nw<DT, 4>(a, grid, stream, paged, uni);
+}
+
+}  // namespace tmla
+
+using namespace tmla;
+
+extern "C" {
+
+const char* tmla_last_error(void) { return g_err; }
+
+int tmla_version(void) { return 100; }
+
+size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v, int32_t num_splits,
+                            int32_t num_workers) {
+  return workspace_bytes(batch, num_heads, head_dim_v, num_splits, num_workers);
+}
+
+int32_t tmla_device_cu_count(int32_t device) {
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
+  return n;
+}
+
+int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                            int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
+                            const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols,
+                            const int32_t* seqlens, int32_t batch, int32_t num_heads, int32_t head_dim_v,
+                            int32_t rope_dim, int32_t dtype, float softmax_scale, int32_t num_splits,
+                            int32_t num_workers, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                            float* lse, void* workspace, size_t workspace_bytes_, void* stream) {
+  const Common c{batch, num_heads, head_dim_v, rope_dim, dtype, num_splits, num_workers};
+  int rc = check_common(c, workspace, workspace_bytes_);
+  if (rc != TMLA_OK) return rc;
+  if (rope_dim != 64) return fail(TMLA_ERR_UNSUPPORTED, "rope_dim must be 64");
+  if (batch == 0) return TMLA_OK;
+  if (!q || !kv || !seqlens || !out || !lse) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (page_size <= 0 || num_blocks <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "page_size and num_blocks must be > 0");
+  const bool paged = block_table != nullptr;
+  if (paged && bt_cols <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "block_table needs at least one column");
+  if (!paged && page_size != 1) return fail(TMLA_ERR_INVALID_ARGUMENT, "dense cache requires page_size == 1");
+  if (((uintptr_t)q | (uintptr_t)kv | (uintptr_t)out) & 15)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "q, kv and out must be 16-byte aligned");
+  if ((q_stride_b | q_stride_h | kv_stride_0 | kv_stride_1 | out_stride_b | out_stride_h) & 7)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "strides must be multiples of 8 elements");
+
+  PartialArgs a{};
+  a.q = static_cast<const char*>(q);
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.kv = static_cast<const char*>(kv);
+  a.kv_s0 = kv_stride_0 * 2;
+  a.kv_s1 = kv_stride_1 * 2;
+  a.num_blocks = num_blocks;
+  a.page_size = page_size;
+  a.page_shift = (page_size & (page_size - 1)) == 0 ? __builtin_ctz((unsigned)page_size) : -1;
+  a.bt = block_table;
+  a.bt_sb = bt_stride_b;
+  a.bt_cols = paged ? bt_cols : 1;
+  a.seqlens = seqlens;
+  a.batch = batch;
+  a.num_heads = num_heads;
+  a.qk_scale_log2 = softmax_scale * kLog2e;
+  a.num_splits = num_splits;
+  a.num_workers = num_workers;
+  a.out = static_cast<char*>(out);
+  a.out_sb = out_stride_b;
+  a.out_sh = out_stride_h;
+  a.lse = lse;
+  char* ws = static_cast<char*>(workspace);
+  const int64_t slots = num_splits > 0 ? (int64_t)batch * num_splits : (int64_t)num_workers + batch;
+  a.mid_o = reinterpret_cast<float*>(ws);
+  a.mid_lse = reinterpret_cast<float*>(ws + (((size_t)slots * num_heads * 512 * 4 + 255) & ~(size_t)255));
+
+  const int nw = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
+  const int heads_per_wg = 32 * nw;
+  const int workers = num_splits > 0 ? batch * num_splits : num_workers;
+  dim3 grid(workers, (num_heads + heads_per_wg - 1) / heads_per_wg);
+  // one page per 32-token sub-tile: sub-tiles never straddle a page
+  const bool uni = paged && (page_size % kSubTokens == 0);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = dtype == TMLA_BF16 ? launch_partial_dt<TMLA_BF16>(a, grid, nw, s, paged, uni)
+                                    : launch_partial_dt<TMLA_FP16>(a, grid, nw, s, paged, uni);
+  if (e != hipSuccess) return hip_fail(e, "mla_partial_kernel launch");
+  return TMLA_OK;
+}
+
+int tmla_mla_decode_combine(const int32_t* seqlens, int32_t batch, int32_t num_heads, int32_t head_dim_v,
+                            int32_t dtype, int32_t num_splits, int32_t num_workers, void* out,
+                            int64_t out_stride_b, int64_t out_stride_h, float* lse, const void* workspace,
+                            size_t workspace_bytes_, void* stream) {
+  const Common c{batch, num_heads, head_dim_v, 64, dtype, num_splits, num_workers};
+  int rc = check_common(c, workspace, workspace_bytes_);
+  if (rc != TMLA_OK) return rc;
+  if (batch == 0) return TMLA_OK;
+  if (!seqlens || !out || !lse) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  CombineArgs a{};
+  a.seqlens = seqlens;
+  a.batch = batch;
+  a.num_heads = num_heads;
+  a.num_splits = num_splits;
+  a.num_workers = num_workers;
+  a.out = static_cast<char*>(out);
+  a.out_sb = out_stride_b;
+  a.out_sh = out_stride_h;
+  a.lse = lse;
+  const char* ws = static_cast<const char*>(workspace);
+  const int64_t slots = num_splits > 0 ? (int64_t)batch * num_splits : (int64_t)num_workers + batch;
+  a.mid_o = reinterpret_cast<const float*>(ws);
+  a.mid_lse = reinterpret_cast<const float*>(ws + (((size_t)slots * num_heads * 512 * 4 + 255) & ~(size_t)255));
+  dim3 grid(batch, (num_heads + 3) / 4);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TMLA_BF16)
+    hipLaunchKernelGGL((mla_combine_kernel<TMLA_BF16, 512>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((mla_combine_kernel<TMLA_FP16, 512>), grid, dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "mla_combine_kernel launch");
+  return TMLA_OK;
+}
+
+int tmla_mla_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv, int64_t kv_stride_0,
+                    int64_t kv_stride_1, int64_t num_blocks, int32_t page_size, const int32_t* block_table,
+                    int64_t bt_stride_b, int32_t bt_cols, const int32_t* seqlens, int32_t batch,
+                    int32_t num_heads, int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale,
+                    int32_t num_splits, int32_t num_workers, void* out, int64_t out_stride_b,
+                    int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes_, void* stream) {
+  int rc = tmla_mla_decode_partial(q, q_stride_b, q_stride_h, kv, kv_stride_0, kv_stride_1, num_blocks, page_size,
+                                   block_table, bt_stride_b, bt_cols, seqlens, batch, num_heads, head_dim_v,
+                                   rope_dim, dtype, softmax_scale, num_splits, num_workers, out, out_stride_b,
+                                   out_stride_h, lse, workspace, workspace_bytes_, stream);
+  if (rc != TMLA_OK) return rc;
+  return tmla_mla_decode_combine(seqlens, batch, num_heads, head_dim_v, dtype, num_splits, num_workers, out,
+                                 out_stride_b, out_stride_h, lse, workspace, workspace_bytes_, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,75 @@
+"""ctypes binding of the C ABI in include/triton_mla.h (libtriton_mla_hip.so).
+
+The library is loaded after torch so that its HIP runtime dependency
+(soname libamdhip64.so.7) resolves to the runtime torch already mapped. There
+is no fallback: if the library is missing or fails to load, every entry point
+that needs it raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtriton_mla_hip.so")
+
+# name -> (restype, argtypes); mirrors include/triton_mla.h
+_i32, _i64, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+_vp, _sz = ctypes.c_void_p, ctypes.c_size_t
+SIGNATURES = {
+    "tmla_last_error": (ctypes.c_char_p, []),
+    "tmla_version": (ctypes.c_int, []),
+    "tmla_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "tmla_device_cu_count": (_i32, [_i32]),
+    "tmla_mla_decode_partial": (ctypes.c_int, [
+        _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
+        _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "tmla_mla_decode_combine": (ctypes.c_int, [
+        _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "tmla_mla_decode": (ctypes.c_int, [
+        _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
+        _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+}
+
+STATUS = {0: "TMLA_OK", 1: "TMLA_ERR_INVALID_ARGUMENT", 2: "TMLA_ERR_UNSUPPORTED",
+          3: "TMLA_ERR_WORKSPACE_TOO_SMALL", 4: "TMLA_ERR_HIP"}
+DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NativeError(RuntimeError):
+    """A C-ABI entry point returned a non-zero tmla_status."""
+
+
+def load():
+    """Load (once) and return the ctypes library; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"triton_mla HIP library not found at {LIB_PATH}; build it with "
+                    "`python triton-mla_amd/build.py` (or __graft_entry__.build())")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().tmla_last_error().decode(errors="replace")
+        kind = STATUS.get(status, str(status))
+        if status in (1, 2):
+            raise ValueError(f"{what}: {kind}: {msg}")
+        raise NativeError(f"{what}: {kind}: {msg}")

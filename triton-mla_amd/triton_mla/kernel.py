@@ -1,0 +1,170 @@
+"""Host side of weight-absorbed MLA decode on MI355X (gfx950).
+
+``mla_decode`` keeps the signature, defaults, validation and return values of
+the reference wrapper (src/triton_mla/kernel.py:204-323). The device work is
+done by the HIP kernels in triton-mla_amd/csrc/mla_decode.hip, called through
+the C ABI in include/triton_mla.h:
+
+  * ``tmla_mla_decode_partial`` -- split-KV partial attention (replaces the
+    reference's stage-1 launch, kernel.py:276-302);
+  * ``tmla_mla_decode_combine`` -- log-sum-exp merge (replaces the stage-2
+    launch, kernel.py:303-320).
+
+Tensors stay on the GPU; there is no CPU or eager fallback. With
+``num_splits=None`` the token-balanced work partition is computed on the
+device from ``cache_seqlens``, so no call synchronises with the host.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+
+_DTYPES = (torch.bfloat16, torch.float16)
+_SUPPORTED_DIMS = {(512, 64)}  # (head_dim_v, rope_dim) with compiled kernels
+
+
+def _next_power_of_2(n: int) -> int:
+    return 1 if n <= 1 else 1 << (n - 1).bit_length()
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def _num_sms(device) -> int:
+    """Compute units of ``device`` (kernel.py:184-187; 132 off-GPU as there)."""
+    device = torch.device(device)
+    if device.type == "cuda":
+        return torch.cuda.get_device_properties(device).multi_processor_count
+    return 132
+
+
+def get_num_splits(batch, num_heads, max_seqlen, num_sms, min_tokens_per_split=128):
+    """Uniform split count of the reference heuristic (kernel.py:190-201).
+
+    Largest power of two <= min(num_sms // (batch * cdiv(num_heads, 64)),
+    cdiv(max_seqlen, min_tokens_per_split), 64), at least 1. Kept bit-for-bit
+    because callers pass its result as ``num_splits``. ``mla_decode`` with
+    ``num_splits=None`` does not use it: it balances tiles over all compute
+    units on the device instead.
+    """
+    head_groups = _cdiv(num_heads, 64)
+    target = num_sms // max(batch * head_groups, 1)
+    max_by_len = _cdiv(max_seqlen, min_tokens_per_split)
+    splits = max(min(target, max_by_len, 64), 1)
+    return 1 << (splits.bit_length() - 1)
+
+
+def _aligned(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:-1])
+
+
+def mla_decode(
+    q: torch.Tensor,
+    kv_cache: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    block_table: torch.Tensor = None,
+    head_dim_v: int = 512,
+    softmax_scale: float = None,
+    num_splits: int = None,
+    return_lse: bool = False,
+):
+    """Weight-absorbed MLA decode attention over a shared latent KV cache.
+
+    Args:
+        q: [batch, num_heads, head_dim_v + rope_dim]; the first head_dim_v dims
+            are the W_UK-absorbed nope query, the rest the RoPE query.
+        kv_cache: paged [num_blocks, page_size, head_dim_v + rope_dim] when
+            block_table is given, otherwise dense [batch, max_seqlen, ...].
+            A singleton kv-head dim ([..., 1, D], FlashMLA layout) is accepted.
+        cache_seqlens: [batch] number of valid tokens per sequence.
+        block_table: optional [batch, max_blocks_per_seq] page indices.
+        head_dim_v: latent rank (512 for DeepSeek-V2/V3).
+        softmax_scale: defaults to q.shape[-1] ** -0.5.
+        num_splits: None (default) spreads the KV tiles of all sequences
+            evenly over the GPU's compute units, computed on the device (no
+            host sync, graph-capturable). An int cuts every sequence into that
+            many tile-aligned pieces, as the reference's split-KV scheme does.
+        return_lse: also return the natural-log log-sum-exp per head.
+
+    Returns:
+        out [batch, num_heads, head_dim_v] in q.dtype (and lse [batch,
+        num_heads] float32).
+    """
+    # validation mirrors kernel.py:235-245
+    if kv_cache.dim() == 4:
+        assert kv_cache.shape[2] == 1, "MLA uses a single shared latent KV head"
+        kv_cache = kv_cache.squeeze(2)
+    assert q.dim() == 3 and kv_cache.dim() == 3
+    batch, num_heads, d_qk = q.shape
+    d_rope = d_qk - head_dim_v
+    assert kv_cache.shape[-1] == d_qk
+    assert q.stride(-1) == 1 and kv_cache.stride(-1) == 1
+    assert _next_power_of_2(head_dim_v) == head_dim_v
+    assert _next_power_of_2(d_rope) == d_rope
+    assert q.dtype == kv_cache.dtype
+
+    if q.device.type != "cuda" or kv_cache.device != q.device:
+        raise RuntimeError("triton_mla.mla_decode runs on the GPU only: q and kv_cache must be "
+                           "on the same HIP device")
+    if q.dtype not in _DTYPES:
+        raise NotImplementedError(f"mla_decode supports bf16 and fp16 inputs, got {q.dtype}")
+    if (head_dim_v, d_rope) not in _SUPPORTED_DIMS:
+        raise NotImplementedError(
+            f"mla_decode kernels are built for head_dim_v=512, rope_dim=64; got {head_dim_v}, {d_rope}")
+    if num_splits is not None:
+        num_splits = int(num_splits)
+        assert num_splits >= 1, "num_splits must be >= 1"
+
+    if softmax_scale is None:
+        softmax_scale = d_qk ** -0.5  # kernel.py:247-248
+    device = q.device
+    cache_seqlens = cache_seqlens.to(device=device, dtype=torch.int32).contiguous()
+    assert cache_seqlens.shape == (batch,), "cache_seqlens must be [batch]"
+
+    paged = block_table is not None
+    if paged:
+        block_table = block_table.to(device=device, dtype=torch.int32)
+        if block_table.stride(-1) != 1:
+            block_table = block_table.contiguous()
+        assert block_table.dim() == 2 and block_table.shape[0] == batch
+        page_size = kv_cache.shape[1]
+        num_blocks = kv_cache.shape[0]
+        bt_ptr, bt_stride, bt_cols = block_table.data_ptr(), block_table.stride(0), block_table.shape[1]
+    else:
+        assert kv_cache.shape[0] == batch  # kernel.py:258
+        page_size = 1
+        num_blocks = kv_cache.shape[1]
+        bt_ptr, bt_stride, bt_cols = None, 0, 1
+
+    out = torch.empty(batch, num_heads, head_dim_v, dtype=q.dtype, device=device)
+    lse = torch.empty(batch, num_heads, dtype=torch.float32, device=device)
+    if batch == 0:
+        return (out, lse) if return_lse else out
+    if num_blocks == 0:
+        raise ValueError("kv_cache holds no tokens")
+    if not _aligned(q):
+        q = q.contiguous()
+    if not _aligned(kv_cache):
+        kv_cache = kv_cache.contiguous()
+
+    lib = _native.load()
+    splits = num_splits if num_splits is not None else 0
+    workers = 0 if num_splits is not None else _num_sms(device)
+    ws_bytes = lib.tmla_workspace_bytes(batch, num_heads, head_dim_v, splits, workers)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        status = lib.tmla_mla_decode(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), num_blocks, page_size,
+            bt_ptr, bt_stride, bt_cols, cache_seqlens.data_ptr(), batch, num_heads, head_dim_v,
+            d_rope, _native.DTYPE_CODE[q.dtype], float(softmax_scale), splits, workers,
+            out.data_ptr(), out.stride(0), out.stride(1), lse.data_ptr(),
+            workspace.data_ptr(), ws_bytes, stream)
+    _native.check(status, "tmla_mla_decode")
+    if return_lse:
+        return out, lse
+    return out

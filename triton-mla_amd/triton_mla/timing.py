@@ -1,0 +1,46 @@
+"""GPU timing helpers: hipEvent-timed repetitions with a cache flush between them.
+
+MI355X has a 256 MiB Infinity Cache in front of HBM, so every timed
+repetition is preceded by a write of ``flush_bytes`` (default 512 MiB) to
+evict the previous repetition's working set.
+"""
+
+from __future__ import annotations
+
+import statistics
+
+import torch
+
+
+class Flusher:
+    def __init__(self, device, flush_bytes: int = 512 << 20):
+        self.buf = torch.empty(max(flush_bytes // 4, 1), dtype=torch.int32, device=device)
+
+    def __call__(self):
+        self.buf.fill_(1)
+
+
+def time_us(fn, reps: int = 100, warmup: int = 5, flush: Flusher | None = None,
+            device=None) -> dict:
+    """Median / mean / min microseconds of ``fn()`` over ``reps`` timed runs.
+
+    Each run is bracketed by events recorded on the current stream of
+    ``device``; the flush (if any) runs before the start event.
+    """
+    device = torch.device(device) if device is not None else torch.device("cuda")
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize(device)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    stream = torch.cuda.current_stream(device)
+    for i in range(reps):
+        if flush is not None:
+            flush()
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    torch.cuda.synchronize(device)
+    times = [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
+    return {"median": statistics.median(times), "mean": statistics.fmean(times), "min": min(times),
+            "reps": reps}
