@@ -1,0 +1,178 @@
+"""Benchmark of the MLA decode hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 100] [--warmup 10]
+
+A step is one mla_decode (split-KV partial kernel + log-sum-exp combine) over
+the measured workload: batch 32, 128 heads, 8192 cached tokens per sequence,
+bf16, page size 64, shuffled block tables, inputs ~ N(0, 1) drawn on the CPU
+with seed 0 and resident in HBM before timing. Every step is preceded by a
+512 MiB write that evicts the 256 MiB Infinity Cache; HIP events on the
+launch stream bracket each kernel.
+
+Prints one JSON line: throughput in TFLOP/s (flops = 2 * H * (576 + 512) per
+cached token), microseconds per step, the HBM roofline of the dominant
+(partial) kernel and the CPU oracle timed on a bounded sample of the same
+workload on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "triton-mla_amd"))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+METRIC = "mla_decode µs/step + TFLOPS (% roofline), B=32 H=128 ctx 8K bf16, 1 GPU"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_b32_h128_ctx8k.json")
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--splits", default="balanced",
+                   help="'balanced' (device-side tile balancing) or an integer split count")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-oracle sample time")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-flush", action="store_true", help="do not evict caches between steps")
+    return p.parse_args()
+
+
+def cpu_baseline(inp, target_s):
+    """Time the float64 CPU oracle (oracle/mla_oracle.c) on the first n sequences."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+
+    def u16(t):
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    q, kv, lens, bt = u16(inp.q), u16(inp.kv_cache), inp.seqlens.numpy(), inp.block_table.numpy()
+
+    def run(n):
+        t0 = time.perf_counter()
+        out, lse = oracle.mla_decode_ref(q[:n], kv, lens[:n], bt[:n], 512, inp.softmax_scale,
+                                         nthreads=threads)
+        return time.perf_counter() - t0, out, lse
+
+    t1, _, _ = run(1)
+    n = int(max(1, min(inp.batch, round(target_s / max(t1, 1e-3)))))
+    t, out, lse = run(n)
+    flops = int(lens[:n].sum()) * inp.heads * 2 * (576 + 512)
+    return {"seconds": t, "sequences": n, "flops": flops, "threads": threads, "out": out, "lse": lse}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              "(the decode path runs and is measured on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from triton_mla import workloads
+    from triton_mla.kernel import DecodeLaunch
+    from triton_mla.timing import Flusher
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inp = workloads.b32_h128_8k().to(dev)
+    splits = None if args.splits == "balanced" else int(args.splits)
+    call = DecodeLaunch(inp.q, inp.kv_cache, inp.seqlens, inp.block_table, 512, inp.softmax_scale, splits)
+    flush = None if args.no_flush else Flusher(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    for _ in range(args.warmup):
+        if flush:
+            flush()
+        call.partial()
+        call.combine()
+    torch.cuda.synchronize(dev)
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize(dev)
+    wall0 = time.perf_counter()
+    for i in range(args.steps):
+        if flush:
+            flush()
+        ev[i][0].record(stream)
+        call.partial()
+        ev[i][1].record(stream)
+        call.combine()
+        ev[i][2].record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - wall0
+
+    step_us = [e[0].elapsed_time(e[2]) * 1e3 for e in ev]
+    partial_us = [e[0].elapsed_time(e[1]) * 1e3 for e in ev]
+    combine_us = [e[1].elapsed_time(e[2]) * 1e3 for e in ev]
+    us = statistics.median(step_us)
+    p_us = statistics.fmean(partial_us)
+
+    nbytes = inp.algorithmic_bytes()
+    flops = inp.flops()
+    tflops = flops / (us * 1e-6) / 1e12
+    achieved_gbs = nbytes / (p_us * 1e-6) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 5),
+        "us_per_step": round(us, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (randn q/cache, randperm block tables, seed 0)",
+        "config": {"workload": inp.name, "batch": inp.batch, "heads": inp.heads, "seq_len": 8192,
+                   "page_size": 64, "num_splits": args.splits, "cache_flush_mib": 0 if args.no_flush else 512},
+        "roofline": {"bound": "hbm", "kernel": "mla_partial_kernel", "achieved": round(achieved_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "algorithmic_bytes": nbytes,
+                     "partial_us_mean": round(p_us, 2), "combine_us_mean": round(statistics.fmean(combine_us), 2),
+                     "step_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "wall_s_timed_region": round(wall, 4),
+    }
+
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(workloads.b32_h128_8k(), args.cpu_seconds)
+        n = cb["sequences"]
+        out_gpu = call.out[:n].float().cpu()
+        err = (out_gpu - torch.from_numpy(cb["out"])).abs().max().item()
+        if not err <= 1e-2:
+            print(f"correctness gate failed: max |gpu - oracle| = {err}", file=sys.stderr)
+            sys.exit(1)
+        cpu_tflops = cb["flops"] / cb["seconds"] / 1e12
+        result["cpu_baseline"] = {
+            "value": round(cpu_tflops, 5), "unit": "TFLOP/s", "cores": cb["threads"], "kind": "port",
+            "sample": f"float64 C oracle (oracle/mla_oracle.c) on the first {n} of 32 sequences "
+                      f"(8192 tokens, 128 heads each): {cb['seconds']:.2f} s",
+            "us_per_step_equiv": round(cb["seconds"] / n * inp.batch * 1e6, 1),
+            "gpu_vs_oracle_max_abs_err": err,
+        }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

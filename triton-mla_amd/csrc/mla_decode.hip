@@ -27,6 +27,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <utility>
+
 #include "triton_mla.h"
 
 namespace tmla {
@@ -46,6 +48,7 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 constexpr int kStages = 4;          // LDS ring depth (3 sub-tiles in flight)
 constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (p <= 2^8)
+constexpr int kPageTable = 3584;     // page ids staged in LDS per window
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -63,6 +66,7 @@ struct PartialArgs {
   int32_t batch, num_heads;
   float qk_scale_log2;
   int32_t num_splits, num_workers;
+  int32_t xcds;            // workgroups are dealt round-robin over this many L2 domains
   char* out;
   int64_t out_sb, out_sh;  // element strides
   float* lse;
@@ -102,6 +106,95 @@ __device__ __forceinline__ void wait_vmcnt() {
 // in VGPRs instead of letting the allocator shuttle blocks between files.
 __device__ __forceinline__ void pin_vgpr(f32x16& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x)); }
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = 0..N-1, so
+// LDS offsets can be instruction immediates.
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// V^T operand fetch. Issued as asm because the builtin carries no alias
+// information and the compiler would otherwise drain every in-flight
+// LDS-DMA copy (vmcnt(0)) before it; completion is awaited with lgkm_wait.
+template <int OFF>
+__device__ __forceinline__ i16x4 ds_read_tr(const char LDS_AS* p) {
+  i16x4 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(p), "i"(OFF));
+  return r;
+}
+
+// K operand fetch (16 bytes per lane), asm for the same reason as
+// ds_read_tr; completion is awaited with lgkm_wait1.
+template <int OFF>
+__device__ __forceinline__ i16x8 ds_read_b128(const char LDS_AS* p) {
+  i16x8 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(p), "i"(OFF));
+  return r;
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait1(i16x8& x) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(x) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait3(i16x8& x, i16x4& y, i16x4& z) {
+  asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(x), "+v"(y), "+v"(z) : "i"(N));
+}
+// Scalar load of one int (uniform address) with no wait; s_wait_i32 waits
+// for every outstanding LDS/scalar operation and ties the value to that point.
+// Issued only where no LDS read that a later lgkmcnt count relies on is
+// older than it, so the out-of-order scalar return cannot satisfy such a wait
+// early.
+__device__ __forceinline__ int s_load_i32(const int32_t* p) {
+  int r;
+  asm volatile("s_load_dword %0, %1, 0x0" : "=s"(r) : "s"(p));
+  return r;
+}
+__device__ __forceinline__ int s_wait_i32(int v) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v));
+  return v;
+}
+
+// One int from LDS (same address in every lane); waits for it.
+__device__ __forceinline__ int ds_read_b32_now(const int LDS_AS* p) {
+  int r;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(p));
+  return r;
+}
+
+// Wait until at most N LDS/scalar-memory operations are outstanding, and tie
+// the two fetched operands to that point.
+template <int N>
+__device__ __forceinline__ void lgkm_wait(i16x4& x, i16x4& y) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "i"(N));
+}
+
+// S^T accumulation in VGPRs (the PV accumulators own every AGPR). After the
+// chain, mfma_vgpr_fence waits out the MFMA result latency before any VALU
+// instruction reads the accumulator.
+template <int DT>
+__device__ __forceinline__ f32x16 mfma_vgpr_first(const i16x8& a, const i16x8& b) {
+  f32x16 d;
+  if constexpr (DT == TMLA_BF16)
+    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+  else
+    asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+template <int DT>
+__device__ __forceinline__ void mfma_vgpr_acc(f32x16& d, const i16x8& a, const i16x8& b) {
+  if constexpr (DT == TMLA_BF16)
+    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  else
+    asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_vgpr_fence(f32x16& d) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(d));
+}
 
 // Workgroup barrier that the compiler treats as a full memory-ordering point
 // but that adds no counter waits of its own: the producer side waits for its
@@ -196,13 +289,22 @@ void mla_partial_kernel(PartialArgs a) {
   constexpr int WAIT2 = 2 * LOADS < 64 ? 2 * LOADS : LOADS;
 
   __shared__ __attribute__((aligned(1024))) char smem[kStages * STAGE];
-  __shared__ int s_scan[256];
+  // start-up prefix sums (balanced mode), then the page table of the window
+  __shared__ int s_aux[kPageTable];
   __shared__ int s_info[4];
+  int* const s_scan = s_aux;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int worker = blockIdx.x;
+  // Logical worker index: consecutive workers (the pieces of one sequence,
+  // which share its Q rows and write neighbouring partial slots) are placed
+  // on the same XCD, since the dispatcher deals workgroups round-robin over
+  // the XCDs and each XCD has its own L2.
+  const int nwg = gridDim.x;
+  const int worker = (a.xcds > 1 && nwg % a.xcds == 0)
+                         ? (int)(blockIdx.x % a.xcds) * (nwg / a.xcds) + (int)(blockIdx.x / a.xcds)
+                         : (int)blockIdx.x;
   const int head_base = blockIdx.y * (kHeadsPerWave * NW) + wave * kHeadsPerWave;
   const int head = head_base + (lane & 31);
   const bool head_ok = head < a.num_heads;
@@ -293,7 +395,7 @@ void mla_partial_kernel(PartialArgs a) {
 
   // ---- segments -----------------------------------------------------------
   int b = b_first;
-  int t_start = tile_lo;       // local tile index within b
+  int t_start = tile_lo;              // local tile index within b
   int remaining = tile_hi - tile_lo;  // tiles left in this worker's range
   int seg_global_off = off_first;     // balanced mode: tile offset of b
 
@@ -321,35 +423,33 @@ void mla_partial_kernel(PartialArgs a) {
       seg.direct = g1 == g2;
     }
 
-    // ---- Q operands for this sequence -------------------------------------
-    i16x8 qop[NKC];
-    {
-      const short* qrow = reinterpret_cast<const short*>(a.q) + (int64_t)b * a.q_sb +
-                          (int64_t)(head_ok ? head : 0) * a.q_sh + 8 * hi;
-#pragma unroll
-      for (int kc = 0; kc < NKC; ++kc) {
-        i16x8 v = *reinterpret_cast<const i16x8*>(qrow + 16 * kc);
-        qop[kc] = head_ok ? v : (i16x8)0;
-      }
-    }
-
     f32x16 acc[NDB];
 #pragma unroll
     for (int d = 0; d < NDB; ++d) acc[d] = (f32x16)0.0f;
     float m_run = -INFINITY;  // base-2 reference max (per head)
     float l_run = 0.0f;       // sum of p over this lane's half of the tokens
+    i16x8 qop[NKC];           // Q^T operands (B of S^T = K . Q^T), loaded below
 
-    // sub-tiles of 32 tokens; the last one may be partially valid and a
-    // trailing fully-invalid half tile is skipped
+    // sub-tiles of 32 tokens; a trailing fully-invalid half tile is skipped
     const int st0 = 2 * seg.t0;
     const int st1 = min(2 * seg.t1, (n_b + kSubTokens - 1) / kSubTokens);
     const int nst = st1 - st0;
 
-    auto issue = [&](int st) {
+    // Page id of a sub-tile (pages of a multiple of 32 tokens hold whole
+    // sub-tiles): a scalar load issued one iteration before the copy that
+    // needs it, so its wait is free when it comes.
+    const int32_t* bt_row = PAGED ? a.bt + (int64_t)b * a.bt_sb : a.bt;
+    auto page_fetch = [&](int st) __attribute__((always_inline)) -> int {
+      return s_load_i32(bt_row + page_slot_of(a, st * kSubTokens));
+    };
+    auto page_ready = [&](int v) __attribute__((always_inline)) -> int {
+      v = s_wait_i32(v);
+      return v < 0 ? 0 : ((int64_t)v >= a.num_blocks ? (int)(a.num_blocks - 1) : v);
+    };
+
+    auto issue = [&](int st, int page) __attribute__((always_inline)) {
       char LDS_AS* stage = (char LDS_AS*)(void LDS_AS*)smem + (st - st0) % kStages * STAGE;
       const int tok_base = st * kSubTokens;
-      int page = 0;
-      if (PAGED && PAGE_UNIFORM) page = load_page(a, b, page_slot_of(a, tok_base));
 #pragma unroll
       for (int i = 0; i < RG_PER_WAVE; ++i) {
         const int rg = wave * RG_PER_WAVE + i;
@@ -366,41 +466,79 @@ void mla_partial_kernel(PartialArgs a) {
       }
     };
 
-    // prologue: up to kStages-1 sub-tiles in flight
-#pragma unroll
-    for (int i = 0; i < kStages - 1; ++i)
-      if (i < nst) issue(st0 + i);
+    const char LDS_AS* ring = (const char LDS_AS*)(const void LDS_AS*)smem;
 
-    for (int i = 0; i < nst; ++i) {
-      const int st = st0 + i;
-      // wait for this wave's copies of sub-tile st, then for everyone's
-      const int ahead = min(nst - 1 - i, kStages - 2);
-      if (PAGED && !PAGE_UNIFORM) {
-        wait_vmcnt<0>();
-      } else if (ahead >= 2) {
-        wait_vmcnt<WAIT2>();
-      } else if (ahead == 1) {
-        wait_vmcnt<LOADS>();
-      } else {
-        wait_vmcnt<0>();
-      }
-      lds_barrier();
-      // the stage read in the previous iteration is free again
-      if (i + kStages - 1 < nst) issue(st + kStages - 1);
+    // One pass over a sub-tile pair: S^T of the sub-tile in kst (DO_S) and
+    // O^T += V^T P^T of the sub-tile in vst (DO_PV), interleaved step by
+    // step so the MFMA pipe alternates between the independent S chain and
+    // the PV accumulators. LDS operands run PD steps ahead; each step waits
+    // with an lgkmcnt that counts exactly the reads issued after its own.
+    constexpr int PD = 2;
+    constexpr int PV_SPLIT = 2 * NDB - 12;  // PV steps before the softmax; 12 after
+    auto pass = [&](auto DOS, auto PVLO, auto PVHI, const char LDS_AS* kst, const char LDS_AS* vst, f32x16& s,
+                    const i16x8 (&pop)[2]) __attribute__((always_inline)) {
+      constexpr bool do_s = decltype(DOS)::value;
+      constexpr int PV0 = decltype(PVLO)::value;  // PV steps [PV0, PV0 + NV) of 2 * NDB
+      constexpr int NS = do_s ? NKC : 0, NV = decltype(PVHI)::value - PV0;
+      constexpr int NSTEPS = NS > NV ? NS : NV;
+      const char LDS_AS* kbase[4] = {kst + k_off[0], kst + k_off[1], kst + k_off[2], kst + k_off[3]};
+      const char LDS_AS* vbase[2][2] = {{vst + v_off[0][0], vst + v_off[0][1]},
+                                        {vst + v_off[1][0], vst + v_off[1][1]}};
+      i16x8 kb[PD + 1];
+      i16x4 vl[PD + 1], vh[PD + 1];
+      auto fetch = [&](auto T) __attribute__((always_inline)) {
+        constexpr int t = decltype(T)::value;
+        if constexpr (t < NS) kb[t % (PD + 1)] = ds_read_b128<(t >> 2) * 1024>(kbase[t & 3]);
+        if constexpr (t < NV) {
+          constexpr int c = (PV0 + t) / NDB, db = (PV0 + t) % NDB;
+          constexpr int off = c * 2 * NCB * 1024 + (db >> 1) * 1024;
+          vl[t % (PD + 1)] = ds_read_tr<off>(vbase[db & 1][0]);
+          vh[t % (PD + 1)] = ds_read_tr<off>(vbase[db & 1][1]);
+        }
+      };
+      static_for<PD>([&](auto T) __attribute__((always_inline)) { fetch(T); });
+      static_for<NSTEPS>([&](auto J) __attribute__((always_inline)) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (j + PD < NSTEPS) fetch(std::integral_constant<int, j + PD>{});
+        // reads issued after those of step j
+        constexpr int last = (j + PD < NSTEPS - 1) ? j + PD : NSTEPS - 1;
+        constexpr int after = [] {
+          int n = 0;
+          for (int t = j + 1; t <= last; ++t) n += (t < NS ? 1 : 0) + (t < NV ? 2 : 0);
+          return n;
+        }();
+        constexpr int r = j % (PD + 1);
+        if constexpr (j < NS && j < NV) {
+          lgkm_wait3<after>(kb[r], vl[r], vh[r]);
+        } else if constexpr (j < NS) {
+          lgkm_wait1<after>(kb[r]);
+        } else {
+          lgkm_wait<after>(vl[r], vh[r]);
+        }
+        if constexpr (j < NS) {
+          if constexpr (j == 0)
+            s = mfma_vgpr_first<DT>(kb[0], qop[0]);
+          else
+            mfma_vgpr_acc<DT>(s, kb[r], qop[j]);
+        }
+        if constexpr (j < NV) {
+          constexpr int c = (PV0 + j) / NDB, db = (PV0 + j) % NDB;
+          const i16x4 lo = vl[r], hi4 = vh[r];
+          const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+          acc[db] = Elt<DT>::mfma(vop, pop[c], acc[db]);
+          pin_agpr(acc[db]);
+        }
+      });
+      if constexpr (do_s) mfma_vgpr_fence(s);
+    };
 
-      const char LDS_AS* stage = (const char LDS_AS*)(const void LDS_AS*)smem + i % kStages * STAGE;
-
-      // ---- S^T = K . Q^T over all DQK dims (32 tokens x 32 heads) --------
-      f32x16 s = (f32x16)0.0f;
-#pragma unroll
-      for (int kc = 0; kc < NKC; ++kc) {
-        const i16x8 kop =
-            *reinterpret_cast<const i16x8 LDS_AS*>(stage + k_off[kc & 3] + (kc >> 2) * 1024);
-        s = Elt<DT>::mfma(kop, qop[kc], s);
-      }
-      pin_vgpr(s);
-
-      // ---- online softmax (base 2) ----------------------------------------
+    // Base-2 online softmax of sub-tile st, in two parts so that the VALU work
+    // overlaps MFMAs. softmax_stats masks tokens past the sequence, scales,
+    // and decides (wave-uniformly) whether the reference max must move: only
+    // when a score exceeds it by 2^kRescaleLog2 (lazy rescale).
+    // softmax_exp then packs p = 2^(x - reference) into the P^T operands.
+    // The O^T rescale itself waits until every earlier PV MFMA was issued.
+    auto softmax_stats = [&](f32x16& s, int st, float& m_use, bool& moved) __attribute__((always_inline)) {
       const int tok0 = st * kSubTokens + 4 * hi;
       float mx = -INFINITY;
 #pragma unroll
@@ -412,48 +550,102 @@ void mla_partial_kernel(PartialArgs a) {
       }
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run, mx);
-      // lazy rescale: move the reference only when a score exceeds it by 2^8
-      const bool need = m_new > m_run + kRescaleLog2;
-      if (__builtin_amdgcn_ballot_w64(need)) {
-        if (m_run != -INFINITY) {
-          const float alpha = fast_exp2(m_run - m_new);
-          l_run *= alpha;
-          // one 16-register block at a time, so the accumulators stay in AGPRs
-#pragma unroll
-          for (int d = 0; d < NDB; ++d) {
-            f32x16 t = acc[d];
-            pin_vgpr(t);
-            t *= alpha;
-            acc[d] = t;
-            pin_agpr(acc[d]);
-          }
-        }
-        m_run = m_new;
-      }
-      i16x8 pop[2];
+      moved = __builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0;
+      m_use = moved ? m_new : m_run;
+    };
+    auto softmax_exp = [&](const f32x16& s, float m_use, i16x8 (&pnext)[2]) __attribute__((always_inline)) -> float {
+      float lsum = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(s[r] - m_run);
-        l_run += p;
-        pop[r >> 3][r & 7] = Elt<DT>::from_float(p);
+        const float p = fast_exp2(s[r] - m_use);
+        lsum += p;
+        pnext[r >> 3][r & 7] = Elt<DT>::from_float(p);
       }
-
-      // ---- O^T += V^T . P^T  (512 dims x 32 heads, k = 32 tokens) --------
+      return lsum;
+    };
+    auto rescale = [&](float m_use) __attribute__((always_inline)) {
+      if (m_run != -INFINITY) {
+        const float alpha = fast_exp2(m_run - m_use);
+        l_run *= alpha;
+        // one 16-register block at a time, so the accumulators stay in AGPRs
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const int base = c * 2 * NCB * 1024 + (db >> 1) * 1024;
-          const i16x4 lo = __builtin_bit_cast(
-              i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                         (i16x4 LDS_AS*)(stage + v_off[db & 1][0] + base)));
-          const i16x4 hi4 = __builtin_bit_cast(
-              i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                         (i16x4 LDS_AS*)(stage + v_off[db & 1][1] + base)));
-          const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-          acc[db] = Elt<DT>::mfma(vop, pop[c], acc[db]);
-          pin_agpr(acc[db]);
+        for (int d = 0; d < NDB; ++d) {
+          f32x16 t = acc[d];
+          pin_vgpr(t);
+          t *= alpha;
+          acc[d] = t;
+          pin_agpr(acc[d]);
         }
+      }
+      m_run = m_use;
+    };
+
+    // Q of this sequence, then the first sub-tiles: both latencies overlap,
+    // and the wait below (Q was issued first, so it has landed once at most the
+    // prologue copies are outstanding) lets the loop use Q with no further
+    // vector-memory wait.
+    {
+      const short* qrow = reinterpret_cast<const short*>(a.q) + (int64_t)b * a.q_sb +
+                          (int64_t)(head_ok ? head : 0) * a.q_sh + 8 * hi;
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) {
+        i16x8 v = *reinterpret_cast<const i16x8*>(qrow + 16 * kc);
+        qop[kc] = head_ok ? v : (i16x8)0;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kStages - 1; ++i)
+      if (i < nst) issue(st0 + i, PAGED && PAGE_UNIFORM ? page_ready(page_fetch(st0 + i)) : 0);
+    if (nst >= 3) {
+      wait_vmcnt<(3 * LOADS < 64 ? 3 * LOADS : 63)>();
+    } else if (nst == 2) {
+      wait_vmcnt<(2 * LOADS < 64 ? 2 * LOADS : 63)>();
+    } else {
+      wait_vmcnt<LOADS>();
+    }
+    int next_page = (PAGED && PAGE_UNIFORM && kStages - 1 < nst) ? page_fetch(st0 + kStages - 1) : 0;
+
+    // Iteration i (-1 <= i < nst): PV(i) from stage i interleaved with S(i+1)
+    // from stage i+1, then the softmax of sub-tile i+1; sub-tiles i+2 and
+    // i+3 are in flight. One instance of the pass serves every iteration:
+    // at i = -1 the PV half runs with P = 0 over the (loaded, finite)
+    // sub-tile 0 and adds exactly nothing; at i = nst-1 the S half reads a
+    // stale stage and its result is discarded.
+    i16x8 pop[2] = {(i16x8)0, (i16x8)0};
+    for (int i = -1; i < nst; ++i) {
+      // sub-tile i+1 must have landed; sub-tile i+2 may still be in flight
+      if (i >= 0 && i + 1 < nst) {
+        if (i + 2 < nst) {
+          wait_vmcnt<LOADS>();
+        } else {
+          wait_vmcnt<0>();
+        }
+      }
+      lds_barrier();
+      // stage (i - 1) % kStages was last read in iteration i - 1
+      if (i >= 0 && i + kStages - 1 < nst) {
+        issue(st0 + i + kStages - 1, PAGED && PAGE_UNIFORM ? page_ready(next_page) : 0);
+        if (PAGED && PAGE_UNIFORM && i + kStages < nst) next_page = page_fetch(st0 + i + kStages);
+      }
+      const char LDS_AS* vst = ring + (i < 0 ? 0 : i % kStages) * STAGE;
+      const char LDS_AS* kst = ring + (i + 1) % kStages * STAGE;
+      // S(i+1) with the first PV_SPLIT steps of PV(i); then the softmax of
+      // sub-tile i+1 beside the remaining PV(i) steps
+      f32x16 s;
+      pass(std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{}, kst, vst, s,
+           pop);
+      float m_use;
+      bool moved;
+      softmax_stats(s, st0 + i + 1, m_use, moved);
+      i16x8 pnext[2];
+      const float lsum = softmax_exp(s, m_use, pnext);
+      pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * NDB>{}, kst,
+           vst, s, pop);
+      if (i + 1 < nst) {
+        if (moved) rescale(m_use);
+        l_run += lsum;
+        pop[0] = pnext[0];
+        pop[1] = pnext[1];
       }
     }
     // all waves must be done with the ring before the next segment refills it
@@ -710,6 +902,7 @@ int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_
   a.qk_scale_log2 = softmax_scale * kLog2e;
   a.num_splits = num_splits;
   a.num_workers = num_workers;
+  a.xcds = 8;  // MI355X: 8 XCDs
   a.out = static_cast<char*>(out);
   a.out_sb = out_stride_b;
   a.out_sh = out_stride_h;

@@ -61,6 +61,115 @@ def _aligned(t: torch.Tensor) -> bool:
     return t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:-1])
 
 
+class DecodeLaunch:
+    """Validated arguments of one ``mla_decode`` call, launchable stage by stage.
+
+    ``mla_decode`` builds one and runs both stages; benchmarks use it to time
+    the partial and combine kernels separately on the same stream.
+    """
+
+    def __init__(self, q, kv_cache, cache_seqlens, block_table=None, head_dim_v=512,
+                 softmax_scale=None, num_splits=None):
+        # validation mirrors kernel.py:235-245
+        if kv_cache.dim() == 4:
+            assert kv_cache.shape[2] == 1, "MLA uses a single shared latent KV head"
+            kv_cache = kv_cache.squeeze(2)
+        assert q.dim() == 3 and kv_cache.dim() == 3
+        batch, num_heads, d_qk = q.shape
+        d_rope = d_qk - head_dim_v
+        assert kv_cache.shape[-1] == d_qk
+        assert q.stride(-1) == 1 and kv_cache.stride(-1) == 1
+        assert _next_power_of_2(head_dim_v) == head_dim_v
+        assert _next_power_of_2(d_rope) == d_rope
+        assert q.dtype == kv_cache.dtype
+
+        if q.device.type != "cuda" or kv_cache.device != q.device:
+            raise RuntimeError("triton_mla.mla_decode runs on the GPU only: q and kv_cache must be "
+                               "on the same HIP device")
+        if q.dtype not in _DTYPES:
+            raise NotImplementedError(f"mla_decode supports bf16 and fp16 inputs, got {q.dtype}")
+        if (head_dim_v, d_rope) not in _SUPPORTED_DIMS:
+            raise NotImplementedError(
+                f"mla_decode kernels are built for head_dim_v=512, rope_dim=64; got {head_dim_v}, {d_rope}")
+        if num_splits is not None:
+            num_splits = int(num_splits)
+            assert num_splits >= 1, "num_splits must be >= 1"
+
+        if softmax_scale is None:
+            softmax_scale = d_qk ** -0.5  # kernel.py:247-248
+        device = q.device
+        cache_seqlens = cache_seqlens.to(device=device, dtype=torch.int32).contiguous()
+        assert cache_seqlens.shape == (batch,), "cache_seqlens must be [batch]"
+
+        if block_table is not None:
+            block_table = block_table.to(device=device, dtype=torch.int32)
+            if block_table.stride(-1) != 1:
+                block_table = block_table.contiguous()
+            assert block_table.dim() == 2 and block_table.shape[0] == batch
+            page_size, num_blocks = kv_cache.shape[1], kv_cache.shape[0]
+            bt_args = (block_table.data_ptr(), block_table.stride(0), block_table.shape[1])
+        else:
+            assert kv_cache.shape[0] == batch  # kernel.py:258
+            page_size, num_blocks = 1, kv_cache.shape[1]
+            bt_args = (None, 0, 1)
+
+        self.device = device
+        self.batch, self.num_heads, self.head_dim_v, self.d_rope = batch, num_heads, head_dim_v, d_rope
+        self.out = torch.empty(batch, num_heads, head_dim_v, dtype=q.dtype, device=device)
+        self.lse = torch.empty(batch, num_heads, dtype=torch.float32, device=device)
+        if batch == 0:
+            return
+        if num_blocks == 0:
+            raise ValueError("kv_cache holds no tokens")
+        if not _aligned(q):
+            q = q.contiguous()
+        if not _aligned(kv_cache):
+            kv_cache = kv_cache.contiguous()
+        # keep every tensor whose address is handed to the kernels alive
+        self._keep = (q, kv_cache, cache_seqlens, block_table)
+        self.lib = _native.load()
+        self.splits = num_splits if num_splits is not None else 0
+        self.workers = 0 if num_splits is not None else _num_sms(device)
+        self.ws_bytes = self.lib.tmla_workspace_bytes(batch, num_heads, head_dim_v, self.splits, self.workers)
+        self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=device)
+        self._partial_args = (
+            q.data_ptr(), q.stride(0), q.stride(1),
+            kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), num_blocks, page_size,
+            *bt_args, cache_seqlens.data_ptr(), batch, num_heads, head_dim_v, d_rope,
+            _native.DTYPE_CODE[q.dtype], float(softmax_scale), self.splits, self.workers,
+            self.out.data_ptr(), self.out.stride(0), self.out.stride(1), self.lse.data_ptr(),
+            self.workspace.data_ptr(), self.ws_bytes)
+        self._combine_args = (
+            cache_seqlens.data_ptr(), batch, num_heads, head_dim_v, _native.DTYPE_CODE[q.dtype],
+            self.splits, self.workers, self.out.data_ptr(), self.out.stride(0), self.out.stride(1),
+            self.lse.data_ptr(), self.workspace.data_ptr(), self.ws_bytes)
+
+    def _stream(self):
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def partial(self):
+        """Stage 1 on the current stream (tmla_mla_decode_partial)."""
+        if self.batch:
+            with torch.cuda.device(self.device):
+                _native.check(self.lib.tmla_mla_decode_partial(*self._partial_args, self._stream()),
+                              "tmla_mla_decode_partial")
+
+    def combine(self):
+        """Stage 2 on the current stream (tmla_mla_decode_combine)."""
+        if self.batch:
+            with torch.cuda.device(self.device):
+                _native.check(self.lib.tmla_mla_decode_combine(*self._combine_args, self._stream()),
+                              "tmla_mla_decode_combine")
+
+    def run(self):
+        """Both stages (tmla_mla_decode)."""
+        if self.batch:
+            with torch.cuda.device(self.device):
+                _native.check(self.lib.tmla_mla_decode(*self._partial_args, self._stream()),
+                              "tmla_mla_decode")
+        return self.out, self.lse
+
+
 def mla_decode(
     q: torch.Tensor,
     kv_cache: torch.Tensor,
@@ -93,78 +202,8 @@ def mla_decode(
         out [batch, num_heads, head_dim_v] in q.dtype (and lse [batch,
         num_heads] float32).
     """
-    # validation mirrors kernel.py:235-245
-    if kv_cache.dim() == 4:
-        assert kv_cache.shape[2] == 1, "MLA uses a single shared latent KV head"
-        kv_cache = kv_cache.squeeze(2)
-    assert q.dim() == 3 and kv_cache.dim() == 3
-    batch, num_heads, d_qk = q.shape
-    d_rope = d_qk - head_dim_v
-    assert kv_cache.shape[-1] == d_qk
-    assert q.stride(-1) == 1 and kv_cache.stride(-1) == 1
-    assert _next_power_of_2(head_dim_v) == head_dim_v
-    assert _next_power_of_2(d_rope) == d_rope
-    assert q.dtype == kv_cache.dtype
-
-    if q.device.type != "cuda" or kv_cache.device != q.device:
-        raise RuntimeError("triton_mla.mla_decode runs on the GPU only: q and kv_cache must be "
-                           "on the same HIP device")
-    if q.dtype not in _DTYPES:
-        raise NotImplementedError(f"mla_decode supports bf16 and fp16 inputs, got {q.dtype}")
-    if (head_dim_v, d_rope) not in _SUPPORTED_DIMS:
-        raise NotImplementedError(
-            f"mla_decode kernels are built for head_dim_v=512, rope_dim=64; got {head_dim_v}, {d_rope}")
-    if num_splits is not None:
-        num_splits = int(num_splits)
-        assert num_splits >= 1, "num_splits must be >= 1"
-
-    if softmax_scale is None:
-        softmax_scale = d_qk ** -0.5  # kernel.py:247-248
-    device = q.device
-    cache_seqlens = cache_seqlens.to(device=device, dtype=torch.int32).contiguous()
-    assert cache_seqlens.shape == (batch,), "cache_seqlens must be [batch]"
-
-    paged = block_table is not None
-    if paged:
-        block_table = block_table.to(device=device, dtype=torch.int32)
-        if block_table.stride(-1) != 1:
-            block_table = block_table.contiguous()
-        assert block_table.dim() == 2 and block_table.shape[0] == batch
-        page_size = kv_cache.shape[1]
-        num_blocks = kv_cache.shape[0]
-        bt_ptr, bt_stride, bt_cols = block_table.data_ptr(), block_table.stride(0), block_table.shape[1]
-    else:
-        assert kv_cache.shape[0] == batch  # kernel.py:258
-        page_size = 1
-        num_blocks = kv_cache.shape[1]
-        bt_ptr, bt_stride, bt_cols = None, 0, 1
-
-    out = torch.empty(batch, num_heads, head_dim_v, dtype=q.dtype, device=device)
-    lse = torch.empty(batch, num_heads, dtype=torch.float32, device=device)
-    if batch == 0:
-        return (out, lse) if return_lse else out
-    if num_blocks == 0:
-        raise ValueError("kv_cache holds no tokens")
-    if not _aligned(q):
-        q = q.contiguous()
-    if not _aligned(kv_cache):
-        kv_cache = kv_cache.contiguous()
-
-    lib = _native.load()
-    splits = num_splits if num_splits is not None else 0
-    workers = 0 if num_splits is not None else _num_sms(device)
-    ws_bytes = lib.tmla_workspace_bytes(batch, num_heads, head_dim_v, splits, workers)
-    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
-    with torch.cuda.device(device):
-        stream = torch.cuda.current_stream(device).cuda_stream
-        status = lib.tmla_mla_decode(
-            q.data_ptr(), q.stride(0), q.stride(1),
-            kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), num_blocks, page_size,
-            bt_ptr, bt_stride, bt_cols, cache_seqlens.data_ptr(), batch, num_heads, head_dim_v,
-            d_rope, _native.DTYPE_CODE[q.dtype], float(softmax_scale), splits, workers,
-            out.data_ptr(), out.stride(0), out.stride(1), lse.data_ptr(),
-            workspace.data_ptr(), ws_bytes, stream)
-    _native.check(status, "tmla_mla_decode")
+    call = DecodeLaunch(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits)
+    out, lse = call.run()
     if return_lse:
         return out, lse
     return out
