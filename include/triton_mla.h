@@ -13,7 +13,7 @@
  * Work partition. Stage 1 runs a grid of workers; each worker owns a
  * contiguous range of 64-token KV tiles and, for every sequence that range
  * touches, writes either the final output (when it covers the whole sequence)
- * or a float32 partial plus a base-2 log-sum-exp into a workspace slot.
+ * or a partial (in the input dtype) plus a base-2 log-sum-exp into a workspace slot.
  * Stage 2 merges the partials of every sequence that was split.
  *   num_splits > 0 : every sequence is cut into num_splits tile-aligned
  *                    pieces, one worker each (the reference's uniform
@@ -52,7 +52,7 @@ int tmla_version(void);
 
 /*
  * Bytes of device workspace tmla_mla_decode / _partial / _combine need:
- * partial outputs (float32 [slots, H, head_dim_v]) and base-2 log-sum-exps
+ * partial outputs (input dtype [slots, H, head_dim_v]) and base-2 log-sum-exps
  * (float32 [slots, H]); slots = batch * num_splits (uniform) or
  * num_workers + batch (balanced).
  */

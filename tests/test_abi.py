@@ -41,9 +41,9 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_workspace_arithmetic(lib):
-    # uniform: batch * splits slots; balanced: workers + batch slots (float32 partial + lse)
+    # uniform: batch * splits slots; balanced: workers + batch slots (16-bit partial + float32 lse)
     def expect(slots, heads, dv=512):
-        o = slots * heads * dv * 4
+        o = slots * heads * dv * 2
         return ((o + 255) // 256) * 256 + slots * heads * 4
 
     assert lib.tmla_workspace_bytes(32, 128, 512, 8, 0) == expect(256, 128)

@@ -207,7 +207,9 @@ def test_empty_inputs(gpu):
 
 
 def test_split_invariance(gpu):
-    """Any split count gives the same result to within fp32 merge rounding."""
+    """Any split count gives the same result to within rounding: split
+    partials are stored in the input dtype, so a split result carries one more
+    bf16 rounding (2^-9 relative per partial) than the unsplit one."""
     from triton_mla import mla_decode
 
     q, kv, seqlens, bt, _ = reference_case(128, True, torch.bfloat16)
@@ -215,6 +217,6 @@ def test_split_invariance(gpu):
     base, base_lse = mla_decode(*args, softmax_scale=SCALE, num_splits=1, return_lse=True)
     for splits in (None, 2, 3, 7, 32, 64):
         out, lse = mla_decode(*args, softmax_scale=SCALE, num_splits=splits, return_lse=True)
-        torch.testing.assert_close(out.float(), base.float(), atol=4e-3, rtol=4e-3)
+        torch.testing.assert_close(out.float(), base.float(), atol=1e-2, rtol=1e-2)
         valid = seqlens.to(gpu) > 0
         torch.testing.assert_close(lse[valid], base_lse[valid], atol=1e-4, rtol=1e-5)

@@ -46,8 +46,26 @@ def build(verbose: bool = False) -> str:
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed ({res.returncode})")
+    check_kernel_stubs(LIB + ".tmp")
     os.replace(LIB + ".tmp", LIB)
     return LIB
+
+
+def check_kernel_stubs(path: str) -> None:
+    """Fail when a kernel's host launch stub is undefined in the library.
+
+    If the host pass of the compiler rejects something in a kernel body (for
+    example a GPU register constraint written directly in it), it drops the
+    kernel silently and leaves its launch stub undefined; the library then
+    fails only when it is loaded.
+    """
+    nm = shutil.which("nm")
+    if nm is None:
+        return
+    res = subprocess.run([nm, "-D", "--undefined-only", path], capture_output=True, text=True)
+    missing = [line.split()[-1] for line in res.stdout.splitlines() if "__device_stub__" in line]
+    if missing:
+        raise RuntimeError("kernels dropped by the host compiler pass: " + ", ".join(missing))
 
 
 if __name__ == "__main__":

@@ -4,22 +4,26 @@
 // Reference behaviour: src/triton_mla/kernel.py (stage 1 kernel.py:43-138,
 // stage 2 kernel.py:141-181, host wrapper kernel.py:204-323).
 //
-// Design (one workgroup = one worker, 64 * NW threads, NW waves of 32 heads):
+// Design (one workgroup = one worker, 64 * NW threads, NW waves, 32 * NW heads):
 //  * Each worker owns a range of 64-token tiles; it walks them as 32-token
-//    sub-tiles through a 4-stage LDS ring. Rows are copied HBM -> LDS with
-//    global_load_lds_dwordx4 (no VGPR staging): one instruction moves eight
-//    full 128-byte lines (8 token rows x 128 bytes) into 1 KiB of LDS.
-//  * Each LDS sub-tile is used twice: as K (all 576 dims) for
-//    S^T = K . Q^T and as V (first 512 dims) for O^T += V^T . P^T, both on
-//    v_mfma_f32_32x32x16_{bf16,f16}. V^T operands come straight from the
-//    row-major tile through ds_read_b64_tr_b16.
-//  * Q stays in VGPRs for the whole range (32 heads x 576 dims per wave);
-//    O^T (32 heads x 512 dims, fp32) lives in accumulation registers.
+//    sub-tiles through LDS rings (V dims: 4 entries, rope dims: 3). Rows are
+//    copied HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging): one
+//    instruction moves eight full 128-byte lines into 1 KiB of LDS; the
+//    copies of sub-tile i+3 are spread over the MFMA steps of iteration i.
+//  * S^T = K . Q^T by head: wave w keeps Q^T of its 32 heads in VGPRs, reads
+//    K (all 576 dims) from LDS and runs the softmax of those heads.
+//  * O^T += V^T . P^T by value dimension: wave w owns DV/NW dims of every
+//    head of the workgroup (fp32 accumulators in AGPRs); P^T and the per-head
+//    rescale factors go through LDS, so each V^T operand (read straight from
+//    the row-major tile with ds_read_b64_tr_b16) feeds NW MFMAs.
+//    Both products run on v_mfma_f32_32x32x16_{bf16,f16}.
 //  * Online softmax in the base-2 domain with a lazy rescale: the running
 //    reference max only moves when a new score exceeds it by more than 2^8,
 //    so probabilities stay <= 256 and the O^T rescale is rare.
-//  * The combine kernel merges per-sequence partials exactly like the
-//    reference's stage 2.
+//  * A worker writes its normalised result through LDS as whole rows: the
+//    final output when it covers a sequence alone, else a partial (input
+//    dtype) and a base-2 log-sum-exp that the combine kernel merges exactly
+//    like the reference's stage 2.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -48,7 +52,6 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 constexpr int kStages = 4;          // LDS ring depth (3 sub-tiles in flight)
 constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (p <= 2^8)
-constexpr int kPageTable = 3584;     // page ids staged in LDS per window
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -70,7 +73,7 @@ struct PartialArgs {
   char* out;
   int64_t out_sb, out_sh;  // element strides
   float* lse;
-  float* mid_o;            // [slots, H, DV]
+  short* mid_o;            // [slots, H, DV] normalised partials, input dtype
   float* mid_lse;          // [slots, H], base-2
 };
 
@@ -81,7 +84,7 @@ struct CombineArgs {
   char* out;
   int64_t out_sb, out_sh;
   float* lse;
-  const float* mid_o;
+  const short* mid_o;
   const float* mid_lse;
 };
 
@@ -106,6 +109,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 // in VGPRs instead of letting the allocator shuttle blocks between files.
 __device__ __forceinline__ void pin_vgpr(f32x16& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x)); }
+// (Operand-constrained asm lives in __device__ helpers only: the host pass
+// of the compiler rejects GPU register constraints inside a kernel body.)
+__device__ __forceinline__ void pin_f2(float& a, float& b) { asm volatile("" : "+v"(a), "+v"(b)); }
+__device__ __forceinline__ void pin_f3(float& a, float& b, float& c) { asm volatile("" : "+v"(a), "+v"(b), "+v"(c)); }
+__device__ __forceinline__ void pin_f8(float* x) {
+  asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]));
+}
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I = 0..N-1, so
 // LDS offsets can be instruction immediates.
@@ -136,14 +146,60 @@ __device__ __forceinline__ i16x8 ds_read_b128(const char LDS_AS* p) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(p), "i"(OFF));
   return r;
 }
+// LDS stores of this kernel's own P^T / factor buffers, as asm so that
+// they keep their place among the asm reads whose lgkmcnt counts they share.
+template <int OFF>
+__device__ __forceinline__ void ds_write_b128(char LDS_AS* p, i16x8 v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(p), "v"(v), "i"(OFF));
+}
+__device__ __forceinline__ void ds_write_b32(char LDS_AS* p, float v) {
+  asm volatile("ds_write_b32 %0, %1" : : "v"(p), "v"(v));
+}
+__device__ __forceinline__ f32x4 ds_read_f32x4(const char LDS_AS* p) {
+  f32x4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(p));
+  return r;
+}
 template <int N>
-__device__ __forceinline__ void lgkm_wait1(i16x8& x) {
+__device__ __forceinline__ void lgkm_tie_f4(f32x4& x) {
   asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(x) : "i"(N));
 }
-template <int N>
-__device__ __forceinline__ void lgkm_wait3(i16x8& x, i16x4& y, i16x4& z) {
-  asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(x), "+v"(y), "+v"(z) : "i"(N));
+
+// Wait until at most N LDS/scalar-memory operations are outstanding and tie
+// the operands fetched for one pass step (K, V^T halves, P^T; each present or
+// not) to that point, so no use of them is scheduled above the wait.
+template <int N, bool HK, bool HV, bool HP>
+__device__ __forceinline__ void lgkm_tie(i16x8& k, i16x4& vl, i16x4& vh, i16x8& p) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt range");
+  if constexpr (HK && HV && HP)
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(k), "+v"(vl), "+v"(vh), "+v"(p) : "i"(N));
+  else if constexpr (HK && HV)
+    asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(k), "+v"(vl), "+v"(vh) : "i"(N));
+  else if constexpr (HK && HP)
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(k), "+v"(p) : "i"(N));
+  else if constexpr (HV && HP)
+    asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(vl), "+v"(vh), "+v"(p) : "i"(N));
+  else if constexpr (HK)
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(k) : "i"(N));
+  else if constexpr (HV)
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(vl), "+v"(vh) : "i"(N));
+  else if constexpr (HP)
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(p) : "i"(N));
 }
+
+// LDS reads issued by fetch(t) of a pass (one K operand per S step; two V^T
+// halves at the first head block of a PV column block, one P^T operand at the
+// first column block of a (token half, head block)).
+template <int NS, int NV, int PV0, int NW>
+constexpr int pass_reads(int t) {
+  int n = t < NS ? 1 : 0;
+  if (t < NV) {
+    const int g = PV0 + t;
+    n += (g % NW == 0 ? 2 : 0) + ((g % 16) / NW == 0 ? 1 : 0);
+  }
+  return n;
+}
+
 // Scalar load of one int (uniform address) with no wait; s_wait_i32 waits
 // for every outstanding LDS/scalar operation and ties the value to that point.
 // Issued only where no LDS read that a later lgkmcnt count relies on is
@@ -157,20 +213,6 @@ __device__ __forceinline__ int s_load_i32(const int32_t* p) {
 __device__ __forceinline__ int s_wait_i32(int v) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v));
   return v;
-}
-
-// One int from LDS (same address in every lane); waits for it.
-__device__ __forceinline__ int ds_read_b32_now(const int LDS_AS* p) {
-  int r;
-  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(p));
-  return r;
-}
-
-// Wait until at most N LDS/scalar-memory operations are outstanding, and tie
-// the two fetched operands to that point.
-template <int N>
-__device__ __forceinline__ void lgkm_wait(i16x4& x, i16x4& y) {
-  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "i"(N));
 }
 
 // S^T accumulation in VGPRs (the PV accumulators own every AGPR). After the
@@ -196,6 +238,12 @@ __device__ __forceinline__ void mfma_vgpr_fence(f32x16& d) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(d));
 }
 
+// One LDS-DMA copy: 16 bytes per lane from `src` into LDS at dst + 16 * lane
+// (global_load_lds_dwordx4; completion counts in vmcnt).
+__device__ __forceinline__ void lds_copy16(const char* src, char LDS_AS* dst) {
+  __builtin_amdgcn_global_load_lds(src, (void LDS_AS*)dst, 16, 0, 0);
+}
+
 // Workgroup barrier that the compiler treats as a full memory-ordering point
 // but that adds no counter waits of its own: the producer side waits for its
 // LDS-DMA copies with wait_vmcnt first.
@@ -212,6 +260,9 @@ struct Elt<TMLA_BF16> {
   __device__ static __forceinline__ short from_float(float x) {
     return __builtin_bit_cast(short, (__bf16)x);
   }
+  __device__ static __forceinline__ float to_float(short x) {
+    return __builtin_bit_cast(float, (unsigned)(unsigned short)x << 16);
+  }
 };
 template <>
 struct Elt<TMLA_FP16> {
@@ -222,6 +273,7 @@ struct Elt<TMLA_FP16> {
   __device__ static __forceinline__ short from_float(float x) {
     return __builtin_bit_cast(short, (_Float16)x);
   }
+  __device__ static __forceinline__ float to_float(short x) { return (float)__builtin_bit_cast(_Float16, x); }
 };
 
 // XOR swizzle of the 16-byte piece index inside an 8-row x 128-byte LDS
@@ -267,36 +319,57 @@ struct Segment {
 // Stage 1: split-KV partial attention
 // ---------------------------------------------------------------------------
 //
-// LDS stage (one 32-token sub-tile): 4 row-groups x NCB column blocks of 1 KiB;
-// block (rg, cb) holds rows 8rg..8rg+7, bytes [128cb, 128cb+128) of each row,
+// LDS layout of one 32-token sub-tile, split by lifetime:
+//  * V part (dims 0..DV-1, read by S and by PV): 4 row-groups x NVB column
+//    blocks of 1 KiB in a kStages-deep ring;
+//  * rope part (dims DV..DQK-1, read by S only): 4 row-groups x NRB blocks in
+//    a ring one entry shorter, since it is dead once S of its sub-tile is done.
+// Block (rg, cb) holds rows 8rg..8rg+7, bytes [128cb, 128cb+128) of each row,
 // 16-byte piece p of row r at position r*8 + (p ^ piece_swizzle(r, rg)).
+//
+// Work split inside a workgroup of NW waves (32*NW heads):
+//  * S and the softmax by head: wave w owns heads 32w..32w+31 (its Q^T lives
+//    in its VGPRs) and writes their probabilities P^T and rescale factors to
+//    LDS;
+//  * O^T += V^T P^T by value dimension: wave w owns dims [w*DV/NW, (w+1)*DV/NW)
+//    of all 32*NW heads, so each V^T operand read from LDS feeds NW MFMAs.
 template <int DT, int DV, int DR, int NW, bool PAGED, bool PAGE_UNIFORM>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(1, 1)))
 void mla_partial_kernel(PartialArgs a) {
   constexpr int DQK = DV + DR;
   static_assert(DQK % 64 == 0 && DV % 64 == 0, "row must be whole 128-byte blocks");
   constexpr int NCB = DQK / 64;           // 128-byte column blocks per row
+  constexpr int NVB = DV / 64;            // ... of which hold V dims
+  constexpr int NRB = NCB - NVB;          // ... and rope dims
   constexpr int NKC = DQK / 16;           // k-chunks of QK^T
   constexpr int NDB = DV / 32;            // 32-dim blocks of PV
-  constexpr int BLOCKS = 4 * NCB;         // 1 KiB blocks per stage
-  constexpr int STAGE = BLOCKS * 1024;
+  constexpr int NDBW = NDB / NW;          // ... owned by one wave
+  constexpr int VSLOT = 4 * NVB * 1024;   // V ring entry
+  constexpr int RSLOT = 4 * NRB * 1024;   // rope ring entry
+  constexpr int kRopeStages = kStages - 1;
+  constexpr int PSLOT = NW * 2 * 1024;    // P^T of one sub-tile: [hb][c][lane] x 16 bytes
+  constexpr int ASLOT = 32 * 4 * 4;       // per-head factors: [head % 32][hb] floats
+  constexpr int OFF_R = kStages * VSLOT;
+  constexpr int OFF_P = OFF_R + kRopeStages * RSLOT;
+  constexpr int OFF_A = OFF_P + 2 * PSLOT;
+  constexpr int SMEM = OFF_A + 2 * ASLOT;
   constexpr int RG_PER_WAVE = 4 / NW;
   constexpr int LOADS = RG_PER_WAVE * NCB;  // DMA instructions per wave per sub-tile
+  constexpr int OPITCH = DV * 2 + 16;        // output staging row pitch (bytes)
   static_assert(NW == 1 || NW == 2 || NW == 4, "waves per workgroup");
+  static_assert(NRB >= 1 && NDB % NW == 0 && NDBW % 2 == 0, "column split");
   static_assert(LOADS < 64, "vmcnt immediate range");
-  // vmcnt is a 6-bit counter: with more than 63 copies outstanding behind the
-  // sub-tile we wait for, wait for a later point instead (over-waiting is safe)
-  constexpr int WAIT2 = 2 * LOADS < 64 ? 2 * LOADS : LOADS;
+  static_assert(NW * 32 * OPITCH <= OFF_P, "output staging fits the rings");
+  static_assert(DV == 512, "one output row = 64 lanes x 8 elements");
 
-  __shared__ __attribute__((aligned(1024))) char smem[kStages * STAGE];
-  // start-up prefix sums (balanced mode), then the page table of the window
-  __shared__ int s_aux[kPageTable];
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
   __shared__ int s_info[4];
-  int* const s_scan = s_aux;
+  int* const s_scan = reinterpret_cast<int*>(smem);  // start-up only, before any copy
+  char LDS_AS* const lds = (char LDS_AS*)(void LDS_AS*)smem;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar LDS bases
   // Logical worker index: consecutive workers (the pieces of one sequence,
   // which share its Q rows and write neighbouring partial slots) are placed
   // on the same XCD, since the dispatcher deals workgroups round-robin over
@@ -311,11 +384,12 @@ void mla_partial_kernel(PartialArgs a) {
   const int hi = lane >> 5;  // which half of the 32-token M block / k slots
 
   // ---- work range -------------------------------------------------------
-  int b_first, tile_lo, tile_hi, off_first, chunk = 0;
+  int b_first, tile_lo, tile_hi, off_first, n_first, chunk = 0;
   if (a.num_splits > 0) {
     const int S = a.num_splits;
     const int b = worker / S, s = worker - b * S;
-    const int nt = tiles_of(a.seqlens[b]);
+    n_first = a.seqlens[b];
+    const int nt = tiles_of(n_first);
     const int spt = (nt + S - 1) / S;
     tile_lo = s * spt;
     tile_hi = min(tile_lo + spt, nt);
@@ -327,8 +401,11 @@ void mla_partial_kernel(PartialArgs a) {
     const int nthreads = 64 * NW;
     const int per = (a.batch + nthreads - 1) / nthreads;
     const int lo_b = min(tid * per, a.batch), hi_b = min(lo_b + per, a.batch);
-    int sum = 0;
-    for (int b = lo_b; b < hi_b; ++b) sum += tiles_of(a.seqlens[b]);
+    // the first length of this thread's chunk stays in a register for the
+    // search below (with batch <= 64 * NW that is the whole chunk)
+    const int len0 = lo_b < hi_b ? a.seqlens[lo_b] : 0;
+    int sum = tiles_of(len0);
+    for (int b = lo_b + 1; b < hi_b; ++b) sum += tiles_of(a.seqlens[b]);
     s_scan[tid] = sum;
     __syncthreads();
     // inclusive scan over the per-thread chunk sums (Hillis-Steele in LDS)
@@ -347,10 +424,12 @@ void mla_partial_kernel(PartialArgs a) {
       int off = s_scan[tid] - sum;  // exclusive prefix of this thread's chunk
       if (off <= lo && lo < off + sum) {
         for (int b = lo_b; b < hi_b; ++b) {
-          const int nt = tiles_of(a.seqlens[b]);
+          const int len = b == lo_b ? len0 : a.seqlens[b];
+          const int nt = tiles_of(len);
           if (lo < off + nt) {
             s_info[0] = b;
             s_info[1] = off;
+            s_info[2] = len;
             break;
           }
           off += nt;
@@ -361,22 +440,29 @@ void mla_partial_kernel(PartialArgs a) {
     if (s_info[0] < 0) return;
     b_first = __builtin_amdgcn_readfirstlane(s_info[0]);
     off_first = __builtin_amdgcn_readfirstlane(s_info[1]);
+    n_first = __builtin_amdgcn_readfirstlane(s_info[2]);
     tile_lo = lo - off_first;  // local to b_first
     tile_hi = min(lo + chunk, total) - off_first;  // may run past b_first
+    __syncthreads();  // the scan lives where the first copies land
   }
   if (tile_lo >= tile_hi) return;
 
-  // per-lane LDS read offsets inside a stage
+  // per-lane LDS read offsets inside a ring entry
   // S^T A operand: token = lane%32 (rg = (lane%32)/8, r = lane%8), piece = 2*(kc%4) + hi
-  int k_off[4];
+  int k_off_v[4], k_off_r[4];
   {
     const int rg = (lane & 31) >> 3, r = lane & 7;
     const int sw = piece_swizzle(r, rg);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) k_off[j] = rg * NCB * 1024 + (r * 8 + ((2 * j + hi) ^ sw)) * 16;
+    for (int j = 0; j < 4; ++j) {
+      const int in_block = (r * 8 + ((2 * j + hi) ^ sw)) * 16;
+      k_off_v[j] = rg * NVB * 1024 + in_block;
+      k_off_r[j] = OFF_R + rg * NRB * 1024 + in_block;
+    }
   }
   // V^T operand via ds_read_b64_tr_b16: group g = lane/16, L = lane%16;
   // read e2 covers tokens 16c + 8e2 + 4(g/2) + L/4, dims 32db + 16(g%2) + 4(L%4).
+  // This wave's dims start at block column (wave * NDBW / 2).
   int v_off[2][2];  // [db&1][e2]
   {
     const int g = lane >> 4, L = lane & 15;
@@ -386,7 +472,8 @@ void mla_partial_kernel(PartialArgs a) {
 #pragma unroll
       for (int e2 = 0; e2 < 2; ++e2) {
         const int piece = 4 * dbp + 2 * (g & 1) + ((L & 3) >> 1);
-        v_off[dbp][e2] = e2 * NCB * 1024 + (r * 8 + (piece ^ piece_swizzle(r, e2))) * 16 + 8 * (L & 1);
+        v_off[dbp][e2] = e2 * NVB * 1024 + wave * (NDBW / 2) * 1024 +
+                         (r * 8 + (piece ^ piece_swizzle(r, e2))) * 16 + 8 * (L & 1);
       }
   }
   // DMA: this lane copies, for each of its wave's row-groups, the piece
@@ -400,7 +487,7 @@ void mla_partial_kernel(PartialArgs a) {
   int seg_global_off = off_first;     // balanced mode: tile offset of b
 
   while (remaining > 0) {
-    const int n_b = a.seqlens[b];
+    const int n_b = b == b_first ? n_first : a.seqlens[b];
     const int nt_b = tiles_of(n_b);
     if (nt_b == 0) {  // only possible in balanced mode between sequences
       ++b;
@@ -423,12 +510,15 @@ void mla_partial_kernel(PartialArgs a) {
       seg.direct = g1 == g2;
     }
 
+    // O^T of this wave's dims: block j4 * NW + hb = dims 32 * j4 (of the
+    // wave's slice) x heads 32 * hb of the workgroup
     f32x16 acc[NDB];
 #pragma unroll
     for (int d = 0; d < NDB; ++d) acc[d] = (f32x16)0.0f;
     float m_run = -INFINITY;  // base-2 reference max (per head)
     float l_run = 0.0f;       // sum of p over this lane's half of the tokens
     i16x8 qop[NKC];           // Q^T operands (B of S^T = K . Q^T), loaded below
+    i16x8 pop[2][NW];         // P^T operands of the sub-tile in PV: [c][hb]
 
     // sub-tiles of 32 tokens; a trailing fully-invalid half tile is skipped
     const int st0 = 2 * seg.t0;
@@ -447,53 +537,79 @@ void mla_partial_kernel(PartialArgs a) {
       return v < 0 ? 0 : ((int64_t)v >= a.num_blocks ? (int)(a.num_blocks - 1) : v);
     };
 
-    auto issue = [&](int st, int page) __attribute__((always_inline)) {
-      char LDS_AS* stage = (char LDS_AS*)(void LDS_AS*)smem + (st - st0) % kStages * STAGE;
+    // Copies of one sub-tile: per-lane source rows (one per row-group of this
+    // wave, already offset to this lane's 16-byte piece), then one
+    // global_load_lds per (row-group, column block).
+    auto copy_src = [&](int st, int page, const char* (&src)[RG_PER_WAVE]) __attribute__((always_inline)) {
       const int tok_base = st * kSubTokens;
 #pragma unroll
-      for (int i = 0; i < RG_PER_WAVE; ++i) {
-        const int rg = wave * RG_PER_WAVE + i;
+      for (int ri = 0; ri < RG_PER_WAVE; ++ri) {
+        const int rg = wave * RG_PER_WAVE + ri;
         const int tok = tok_base + rg * 8 + dma_r;
         int pg = page;
         if (PAGED && !PAGE_UNIFORM) pg = load_page(a, b, page_slot_of(a, min(tok, n_b - 1)));
-        const char* row = a.kv + row_offset<PAGED>(a, b, tok, n_b, pg);
-        const int piece = (lane & 7) ^ piece_swizzle(dma_r, rg);
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-          __builtin_amdgcn_global_load_lds(row + cb * 128 + piece * 16,
-                                           (void LDS_AS*)(stage + (rg * NCB + cb) * 1024), 16, 0, 0);
-        }
+        src[ri] = a.kv + row_offset<PAGED>(a, b, tok, n_b, pg) + ((lane & 7) ^ piece_swizzle(dma_r, rg)) * 16;
       }
     };
-
-    const char LDS_AS* ring = (const char LDS_AS*)(const void LDS_AS*)smem;
+    auto copy_one = [&](int st, int ri, int cb, const char* const (&src)[RG_PER_WAVE]) __attribute__((always_inline)) {
+      const int rg = wave * RG_PER_WAVE + ri;
+      char LDS_AS* dst = cb < NVB ? lds + (st - st0) % kStages * VSLOT + (rg * NVB + cb) * 1024
+                                  : lds + OFF_R + (st - st0) % kRopeStages * RSLOT + (rg * NRB + cb - NVB) * 1024;
+      lds_copy16(src[ri] + cb * 128, dst);
+    };
+    auto issue = [&](int st, int page) __attribute__((always_inline)) {
+      const char* src[RG_PER_WAVE];
+      copy_src(st, page, src);
+#pragma unroll
+      for (int ri = 0; ri < RG_PER_WAVE; ++ri)
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) copy_one(st, ri, cb, src);
+    };
 
     // One pass over a sub-tile pair: S^T of the sub-tile in kst (DO_S) and
-    // O^T += V^T P^T of the sub-tile in vst (DO_PV), interleaved step by
-    // step so the MFMA pipe alternates between the independent S chain and
-    // the PV accumulators. LDS operands run PD steps ahead; each step waits
-    // with an lgkmcnt that counts exactly the reads issued after its own.
+    // PV steps [PV0, PV1) of O^T += V^T P^T for the sub-tile in vst,
+    // interleaved step by step so the MFMA pipe alternates between the
+    // independent S chain and the PV accumulators. PV step g is MFMA
+    // (c, j4, hb) = (g / 16, (g % 16) / NW, g % NW); its V^T operand is read
+    // at the first hb of each j4 and its P^T operand at the first j4 of each
+    // c. LDS operands run PD steps ahead; each step waits with an lgkmcnt
+    // that counts exactly the reads issued after its own. hook(step) runs
+    // after each step's MFMAs (copies of a later sub-tile, softmax pieces),
+    // so its VALU and memory work overlaps them.
     constexpr int PD = 2;
-    constexpr int PV_SPLIT = 2 * NDB - 12;  // PV steps before the softmax; 12 after
-    auto pass = [&](auto DOS, auto PVLO, auto PVHI, const char LDS_AS* kst, const char LDS_AS* vst, f32x16& s,
-                    const i16x8 (&pop)[2]) __attribute__((always_inline)) {
+    constexpr int PV_SPLIT = 16;  // PV steps beside S; the rest beside the softmax
+    static_assert(PV_SPLIT % NW == 0 && PV_SPLIT >= 16, "a V^T operand never spans the two passes");
+    auto pass = [&](auto DOS, auto PVLO, auto PVHI, const char LDS_AS* kst_v, const char LDS_AS* kst_r,
+                    const char LDS_AS* vst, const char LDS_AS* pst, f32x16& s, auto&& hook)
+                    __attribute__((always_inline)) {
       constexpr bool do_s = decltype(DOS)::value;
-      constexpr int PV0 = decltype(PVLO)::value;  // PV steps [PV0, PV0 + NV) of 2 * NDB
+      constexpr int PV0 = decltype(PVLO)::value;
       constexpr int NS = do_s ? NKC : 0, NV = decltype(PVHI)::value - PV0;
       constexpr int NSTEPS = NS > NV ? NS : NV;
-      const char LDS_AS* kbase[4] = {kst + k_off[0], kst + k_off[1], kst + k_off[2], kst + k_off[3]};
+      const char LDS_AS* kvb[4] = {kst_v + k_off_v[0], kst_v + k_off_v[1], kst_v + k_off_v[2], kst_v + k_off_v[3]};
+      const char LDS_AS* krb[4] = {kst_r + k_off_r[0], kst_r + k_off_r[1], kst_r + k_off_r[2], kst_r + k_off_r[3]};
       const char LDS_AS* vbase[2][2] = {{vst + v_off[0][0], vst + v_off[0][1]},
                                         {vst + v_off[1][0], vst + v_off[1][1]}};
+      const char LDS_AS* pbase = pst + lane * 16;
       i16x8 kb[PD + 1];
-      i16x4 vl[PD + 1], vh[PD + 1];
+      i16x4 vl[NDBW * 2], vh[NDBW * 2];  // indexed by V^T operand id c * NDBW + j4
       auto fetch = [&](auto T) __attribute__((always_inline)) {
         constexpr int t = decltype(T)::value;
-        if constexpr (t < NS) kb[t % (PD + 1)] = ds_read_b128<(t >> 2) * 1024>(kbase[t & 3]);
+        if constexpr (t < NS) {
+          constexpr int cb = t >> 2;
+          if constexpr (cb < NVB)
+            kb[t % (PD + 1)] = ds_read_b128<cb * 1024>(kvb[t & 3]);
+          else
+            kb[t % (PD + 1)] = ds_read_b128<(cb - NVB) * 1024>(krb[t & 3]);
+        }
         if constexpr (t < NV) {
-          constexpr int c = (PV0 + t) / NDB, db = (PV0 + t) % NDB;
-          constexpr int off = c * 2 * NCB * 1024 + (db >> 1) * 1024;
-          vl[t % (PD + 1)] = ds_read_tr<off>(vbase[db & 1][0]);
-          vh[t % (PD + 1)] = ds_read_tr<off>(vbase[db & 1][1]);
+          constexpr int g = PV0 + t, c = g / 16, j4 = (g % 16) / NW, hb = g % NW;
+          if constexpr (hb == 0) {
+            constexpr int off = c * 2 * NVB * 1024 + (j4 >> 1) * 1024;
+            vl[c * NDBW + j4] = ds_read_tr<off>(vbase[j4 & 1][0]);
+            vh[c * NDBW + j4] = ds_read_tr<off>(vbase[j4 & 1][1]);
+          }
+          if constexpr (j4 == 0) pop[c][hb] = ds_read_b128<(hb * 2 + c) * 1024>(pbase);
         }
       };
       static_for<PD>([&](auto T) __attribute__((always_inline)) { fetch(T); });
@@ -504,17 +620,19 @@ void mla_partial_kernel(PartialArgs a) {
         constexpr int last = (j + PD < NSTEPS - 1) ? j + PD : NSTEPS - 1;
         constexpr int after = [] {
           int n = 0;
-          for (int t = j + 1; t <= last; ++t) n += (t < NS ? 1 : 0) + (t < NV ? 2 : 0);
+          for (int t = j + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NW>(t);
           return n;
         }();
+        constexpr int g = PV0 + (j < NV ? j : 0), c = g / 16, j4 = (g % 16) / NW, hb = g % NW;
+        constexpr bool has_k = j < NS;
+        constexpr bool has_v = j < NV && hb == 0;
+        constexpr bool has_p = j < NV && j4 == 0;
+        constexpr int vi = c * NDBW + j4;
         constexpr int r = j % (PD + 1);
-        if constexpr (j < NS && j < NV) {
-          lgkm_wait3<after>(kb[r], vl[r], vh[r]);
-        } else if constexpr (j < NS) {
-          lgkm_wait1<after>(kb[r]);
-        } else {
-          lgkm_wait<after>(vl[r], vh[r]);
-        }
+        // the wait ties the operands read for this step to it (a step that
+        // only reuses operands needs none)
+        if constexpr (has_k || has_v || has_p)
+          lgkm_tie<after, has_k, has_v, has_p>(kb[r], vl[vi], vh[vi], pop[c][hb]);
         if constexpr (j < NS) {
           if constexpr (j == 0)
             s = mfma_vgpr_first<DT>(kb[0], qop[0]);
@@ -522,68 +640,53 @@ void mla_partial_kernel(PartialArgs a) {
             mfma_vgpr_acc<DT>(s, kb[r], qop[j]);
         }
         if constexpr (j < NV) {
-          constexpr int c = (PV0 + j) / NDB, db = (PV0 + j) % NDB;
-          const i16x4 lo = vl[r], hi4 = vh[r];
+          const i16x4 lo = vl[vi], hi4 = vh[vi];
           const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-          acc[db] = Elt<DT>::mfma(vop, pop[c], acc[db]);
-          pin_agpr(acc[db]);
+          acc[j4 * NW + hb] = Elt<DT>::mfma(vop, pop[c][hb], acc[j4 * NW + hb]);
+          pin_agpr(acc[j4 * NW + hb]);
         }
+        hook(J);
       });
       if constexpr (do_s) mfma_vgpr_fence(s);
     };
 
-    // Base-2 online softmax of sub-tile st, in two parts so that the VALU work
-    // overlaps MFMAs. softmax_stats masks tokens past the sequence, scales,
-    // and decides (wave-uniformly) whether the reference max must move: only
-    // when a score exceeds it by 2^kRescaleLog2 (lazy rescale).
-    // softmax_exp then packs p = 2^(x - reference) into the P^T operands.
-    // The O^T rescale itself waits until every earlier PV MFMA was issued.
-    auto softmax_stats = [&](f32x16& s, int st, float& m_use, bool& moved) __attribute__((always_inline)) {
-      const int tok0 = st * kSubTokens + 4 * hi;
-      float mx = -INFINITY;
+    // PV side: O^T columns of head block hb scale by the factor its S-owner
+    // published; one 16-register block at a time, so the accumulators stay
+    // in AGPRs.
+    auto rescale = [&](const f32x4& alpha4) __attribute__((always_inline)) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tok = tok0 + 8 * (r >> 2) + (r & 3);
-        const float x = tok < n_b ? s[r] * a.qk_scale_log2 : -INFINITY;
-        s[r] = x;
-        mx = fmaxf(mx, x);
+      for (int d = 0; d < NDB; ++d) {
+        f32x16 t = acc[d];
+        pin_vgpr(t);
+        t *= alpha4[d % NW];
+        acc[d] = t;
+        pin_agpr(acc[d]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      moved = __builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0;
-      m_use = moved ? m_new : m_run;
-    };
-    auto softmax_exp = [&](const f32x16& s, float m_use, i16x8 (&pnext)[2]) __attribute__((always_inline)) -> float {
-      float lsum = 0.0f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(s[r] - m_use);
-        lsum += p;
-        pnext[r >> 3][r & 7] = Elt<DT>::from_float(p);
-      }
-      return lsum;
-    };
-    auto rescale = [&](float m_use) __attribute__((always_inline)) {
-      if (m_run != -INFINITY) {
-        const float alpha = fast_exp2(m_run - m_use);
-        l_run *= alpha;
-        // one 16-register block at a time, so the accumulators stay in AGPRs
-#pragma unroll
-        for (int d = 0; d < NDB; ++d) {
-          f32x16 t = acc[d];
-          pin_vgpr(t);
-          t *= alpha;
-          acc[d] = t;
-          pin_agpr(acc[d]);
-        }
-      }
-      m_run = m_use;
     };
 
-    // Q of this sequence, then the first sub-tiles: both latencies overlap,
-    // and the wait below (Q was issued first, so it has landed once at most the
-    // prologue copies are outstanding) lets the loop use Q with no further
-    // vector-memory wait.
+    // P^T (and factor) buffers of the sub-tile before the first: P = 0 and
+    // factor 1, so that iteration -1's PV half adds exactly nothing.
+    {
+      char LDS_AS* p1 = lds + OFF_P + PSLOT + wave * 2 * 1024 + lane * 16;
+      ds_write_b128<0>(p1, (i16x8)0);
+      ds_write_b128<1024>(p1, (i16x8)0);
+      ds_write_b32(lds + OFF_A + ASLOT + ((lane & 31) * 4 + wave) * 4, 1.0f);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+
+    // Start-up, in the order the first iteration needs the data: page ids of
+    // the first kStages sub-tiles (scalar loads, issued before any vector
+    // traffic so they do not queue behind it; one wait), the copy of
+    // sub-tile 0, Q of this sequence, then the copies of sub-tiles 1 and 2.
+    static_assert(kStages == 4, "prologue page ids");
+    int pro_page[kStages] = {0, 0, 0, 0};
+    if (PAGED && PAGE_UNIFORM) {
+#pragma unroll
+      for (int i = 0; i < kStages; ++i) pro_page[i] = page_fetch(st0 + min(i, nst - 1));
+#pragma unroll
+      for (int i = 0; i < kStages; ++i) pro_page[i] = page_ready(pro_page[i]);
+    }
+    issue(st0, pro_page[0]);  // nst >= 1
     {
       const short* qrow = reinterpret_cast<const short*>(a.q) + (int64_t)b * a.q_sb +
                           (int64_t)(head_ok ? head : 0) * a.q_sh + 8 * hi;
@@ -594,24 +697,30 @@ void mla_partial_kernel(PartialArgs a) {
       }
     }
 #pragma unroll
-    for (int i = 0; i < kStages - 1; ++i)
-      if (i < nst) issue(st0 + i, PAGED && PAGE_UNIFORM ? page_ready(page_fetch(st0 + i)) : 0);
+    for (int i = 1; i < kStages - 1; ++i)
+      if (i < nst) issue(st0 + i, pro_page[i]);
+    // sub-tile 0 and Q have landed once at most the later copies are
+    // outstanding (vector loads complete in issue order); the loop then uses Q
+    // with no further wait
     if (nst >= 3) {
-      wait_vmcnt<(3 * LOADS < 64 ? 3 * LOADS : 63)>();
-    } else if (nst == 2) {
       wait_vmcnt<(2 * LOADS < 64 ? 2 * LOADS : 63)>();
-    } else {
+    } else if (nst == 2) {
       wait_vmcnt<LOADS>();
+    } else {
+      wait_vmcnt<0>();
     }
-    int next_page = (PAGED && PAGE_UNIFORM && kStages - 1 < nst) ? page_fetch(st0 + kStages - 1) : 0;
+    int next_page = pro_page[kStages - 1];  // already waited for
 
-    // Iteration i (-1 <= i < nst): PV(i) from stage i interleaved with S(i+1)
-    // from stage i+1, then the softmax of sub-tile i+1; sub-tiles i+2 and
-    // i+3 are in flight. One instance of the pass serves every iteration:
-    // at i = -1 the PV half runs with P = 0 over the (loaded, finite)
-    // sub-tile 0 and adds exactly nothing; at i = nst-1 the S half reads a
-    // stale stage and its result is discarded.
-    i16x8 pop[2] = {(i16x8)0, (i16x8)0};
+    // Iteration i (-1 <= i < nst): PV(i) from ring entry i interleaved with
+    // S(i+1) from entry i+1 (and the copies of sub-tile i+3), then the rest
+    // of PV(i) interleaved with the softmax of sub-tile i+1, which publishes
+    // P^T(i+1) and the factors for the next iteration; sub-tiles i+2 and i+3
+    // are in flight. One instance of the passes serves every iteration: at
+    // i = -1 the PV half multiplies sub-tile 0 by P = 0 and adds exactly
+    // nothing; at i = nst-1 the S half reads a stale entry and its result is
+    // discarded.
+    constexpr int COPY_STRIDE = NKC / LOADS;  // S steps per copy instruction
+    static_assert(NKC % LOADS == 0, "copies spread evenly over the S steps");
     for (int i = -1; i < nst; ++i) {
       // sub-tile i+1 must have landed; sub-tile i+2 may still be in flight
       if (i >= 0 && i + 1 < nst) {
@@ -621,34 +730,108 @@ void mla_partial_kernel(PartialArgs a) {
           wait_vmcnt<0>();
         }
       }
+      const bool do_copy = i >= 0 && i + kStages - 1 < nst;  // sub-tile i+3
+      const int page = (PAGED && PAGE_UNIFORM && do_copy) ? page_ready(next_page) : 0;
+      // every wave's P^T(i) and factors are written and every wave is done
+      // with the ring entries refilled during this iteration
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       lds_barrier();
-      // stage (i - 1) % kStages was last read in iteration i - 1
-      if (i >= 0 && i + kStages - 1 < nst) {
-        issue(st0 + i + kStages - 1, PAGED && PAGE_UNIFORM ? page_ready(next_page) : 0);
-        if (PAGED && PAGE_UNIFORM && i + kStages < nst) next_page = page_fetch(st0 + i + kStages);
+      const int pbuf = i & 1;
+      f32x4 alpha4 = ds_read_f32x4(lds + OFF_A + pbuf * ASLOT + (lane & 31) * 16);
+      const char* csrc[RG_PER_WAVE];
+      if (do_copy) copy_src(st0 + i + kStages - 1, page, csrc);
+      lgkm_tie_f4<0>(alpha4);
+      // issued after the last counted LDS wait before the passes, so its
+      // out-of-order return can only make later waits wait longer
+      if (PAGED && PAGE_UNIFORM && i >= 0 && i + kStages < nst) next_page = page_fetch(st0 + i + kStages);
+      {
+        bool any = false;
+#pragma unroll
+        for (int hb = 0; hb < NW; ++hb) any |= alpha4[hb] != 1.0f;
+        if (__builtin_amdgcn_ballot_w64(any) != 0) rescale(alpha4);
       }
-      const char LDS_AS* vst = ring + (i < 0 ? 0 : i % kStages) * STAGE;
-      const char LDS_AS* kst = ring + (i + 1) % kStages * STAGE;
-      // S(i+1) with the first PV_SPLIT steps of PV(i); then the softmax of
-      // sub-tile i+1 beside the remaining PV(i) steps
+      const char LDS_AS* vst = lds + (i < 0 ? 0 : i % kStages) * VSLOT;
+      const char LDS_AS* kst_v = lds + (i + 1) % kStages * VSLOT;
+      const char LDS_AS* kst_r = lds + (i + 1) % kRopeStages * RSLOT;
+      const char LDS_AS* pst = lds + OFF_P + pbuf * PSLOT;
+      const int st_s = st0 + i + 1;  // sub-tile of this iteration's S
+
+      // pass 1: S(i+1) and PV(i) steps [0, PV_SPLIT), with the copies of
+      // sub-tile i+3 spread over the S steps
+      auto copy_hook = [&](auto J) __attribute__((always_inline)) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (j % COPY_STRIDE == COPY_STRIDE / 2 && j / COPY_STRIDE < LOADS) {
+          constexpr int idx = j / COPY_STRIDE;
+          if (do_copy) copy_one(st0 + i + kStages - 1, idx / NCB, idx % NCB, csrc);
+        }
+      };
       f32x16 s;
-      pass(std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{}, kst, vst, s,
-           pop);
-      float m_use;
-      bool moved;
-      softmax_stats(s, st0 + i + 1, m_use, moved);
+      pass(std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{}, kst_v, kst_r,
+           vst, pst, s, copy_hook);
+
+      // pass 2: PV(i) steps [PV_SPLIT, 2 * NDB) beside the softmax of
+      // sub-tile i+1 (heads of this wave), base-2 with the lazy rescale: the
+      // reference max only moves, for the whole wave, when a score exceeds
+      // it by 2^kRescaleLog2 (then both token halves of every head agree on
+      // the new max through one lane exchange).
+      const bool full = (st_s + 1) * kSubTokens <= n_b;  // no token past the sequence
+      float x[16];
+      float m_use = m_run, lsum = 0.0f, alpha = 1.0f;
       i16x8 pnext[2];
-      const float lsum = softmax_exp(s, m_use, pnext);
-      pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * NDB>{}, kst,
-           vst, s, pop);
+      auto softmax_hook = [&](auto J) __attribute__((always_inline)) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (j < 2) {  // scale (and mask) 8 scores
+          if (full) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[8 * j + e] = s[8 * j + e] * a.qk_scale_log2;
+          } else {
+            const int tok0 = st_s * kSubTokens + 4 * hi;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int r = 8 * j + e;
+              x[r] = tok0 + 8 * (r >> 2) + (r & 3) < n_b ? s[r] * a.qk_scale_log2 : -INFINITY;
+            }
+          }
+          pin_f8(&x[8 * j]);
+        } else if constexpr (j == 2) {  // reference max
+          float mx = x[0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, x[r]);
+          if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleLog2) != 0) {
+            // the exchange is an LDS operation outside the pass's
+            // counting: let every counted read finish first
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            m_use = fmaxf(m_run, fmaxf(mx, __shfl_xor(mx, 32)));
+            if (m_run != -INFINITY) alpha = fast_exp2(m_run - m_use);
+          }
+          pin_f2(m_use, alpha);
+        } else if constexpr (j >= 3 && j < 11) {  // two probabilities
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int r = 2 * (j - 3) + e;
+            x[r] = fast_exp2(x[r] - m_use);
+            lsum += x[r];
+          }
+          pin_f3(x[2 * (j - 3)], x[2 * (j - 3) + 1], lsum);
+        } else if constexpr (j == 11) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) pnext[r >> 3][r & 7] = Elt<DT>::from_float(x[r]);
+        }
+      };
+      pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * NDB>{}, kst_v,
+           kst_r, vst, pst, s, softmax_hook);
+      {
+        char LDS_AS* pw = lds + OFF_P + (pbuf ^ 1) * PSLOT + wave * 2 * 1024 + lane * 16;
+        ds_write_b128<0>(pw, pnext[0]);
+        ds_write_b128<1024>(pw, pnext[1]);
+        ds_write_b32(lds + OFF_A + (pbuf ^ 1) * ASLOT + ((lane & 31) * 4 + wave) * 4, alpha);
+      }
       if (i + 1 < nst) {
-        if (moved) rescale(m_use);
-        l_run += lsum;
-        pop[0] = pnext[0];
-        pop[1] = pnext[1];
+        l_run = l_run * alpha + lsum;
+        m_run = m_use;
       }
     }
-    // all waves must be done with the ring before the next segment refills it
+    // all waves must be done with the rings before they are reused below
     lds_barrier();
 
     // ---- finalize: out = acc / l, lse2 = m + log2(l) -------------------------
@@ -656,32 +839,57 @@ void mla_partial_kernel(PartialArgs a) {
     const bool has = l_tot > 0.0f;
     const float inv = has ? 1.0f / l_tot : 0.0f;
     const float lse2 = has ? m_run + fast_log2(l_tot) : -INFINITY;
-    if (head_ok) {
-      if (seg.direct) {
-        short* orow = reinterpret_cast<short*>(a.out) + (int64_t)b * a.out_sb + (int64_t)head * a.out_sh;
+    {
+      // 1/l of every head of the workgroup, for the waves' column slices
+      ds_write_b32(lds + OFF_A + ((lane & 31) * 4 + wave) * 4, inv);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      lds_barrier();
+      f32x4 inv4 = ds_read_f32x4(lds + OFF_A + (lane & 31) * 16);
+      lgkm_tie_f4<0>(inv4);
+      // The normalised rows go through the idle rings (32*NW padded rows;
+      // the 16-byte pad spreads the lanes' 8-byte writes over all banks),
+      // so that every global store then writes one whole row of DV elements.
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+      for (int j4 = 0; j4 < NDBW; ++j4)
+#pragma unroll
+        for (int hb = 0; hb < NW; ++hb)
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
             i16x4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = Elt<DT>::from_float(acc[db][4 * q4 + e] * inv);
-            *reinterpret_cast<i16x4*>(orow + 32 * db + 8 * q4 + 4 * hi) = v;
+            for (int e = 0; e < 4; ++e) v[e] = Elt<DT>::from_float(acc[j4 * NW + hb][4 * q4 + e] * inv4[hb]);
+            const int dim = wave * (DV / NW) + 32 * j4 + 8 * q4 + 4 * hi;
+            *reinterpret_cast<i16x4 LDS_AS*>(lds + (hb * 32 + (lane & 31)) * OPITCH + dim * 2) = v;
           }
-        if (hi == 0) a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      lds_barrier();
+      short* dst;
+      int64_t row_stride;
+      if (seg.direct) {
+        dst = reinterpret_cast<short*>(a.out) + (int64_t)b * a.out_sb + (int64_t)head_base * a.out_sh;
+        row_stride = a.out_sh;
       } else {
-        float* orow = a.mid_o + ((int64_t)seg.slot * a.num_heads + head) * DV;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            f32x4 v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[db][4 * q4 + e] * inv;
-            *reinterpret_cast<f32x4*>(orow + 32 * db + 8 * q4 + 4 * hi) = v;
-          }
-        if (hi == 0) a.mid_lse[(int64_t)seg.slot * a.num_heads + head] = lse2;
+        // the partial is a convex combination of cache rows, so it fits the
+        // input dtype; it is stored there (half the bytes of float32)
+        dst = a.mid_o + ((int64_t)seg.slot * a.num_heads + head_base) * DV;
+        row_stride = DV;
       }
+      const int rows = min(32, a.num_heads - head_base);  // wave-uniform
+      const char LDS_AS* obuf = lds + wave * 32 * OPITCH;
+#pragma unroll
+      for (int r = 0; r < 32; ++r)
+        if (r < rows)
+          *reinterpret_cast<i16x8*>(dst + r * row_stride + lane * 8) =
+              *reinterpret_cast<const i16x8 LDS_AS*>(obuf + r * OPITCH + lane * 16);
+      if (head_ok && hi == 0) {
+        if (seg.direct)
+          a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
+        else
+          a.mid_lse[(int64_t)seg.slot * a.num_heads + head] = lse2;
+      }
+      // the next segment refills the rings
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      lds_barrier();
     }
 
     remaining -= (t_end - t_start);
@@ -753,27 +961,35 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
   for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
   if (m == -INFINITY) m = 0.0f;
 
+  // Eight partial rows in flight per batch: all loads of a batch are issued
+  // before any is consumed.
+  constexpr int BATCH = 8;
   for (int d0 = 0; d0 < DV; d0 += 512) {
-    f32x4 acc0 = (f32x4)0.0f, acc1 = (f32x4)0.0f;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float wsum = 0.0f;
-    for (int s = 0; s < count; ++s) {
-      const int64_t row = (int64_t)(slot0 + s) * a.num_heads + head;
-      const float w = fast_exp2(a.mid_lse[row] - m);
-      wsum += w;
-      if (w > 0.0f) {  // empty splits carry lse -inf and no partial data
-        const float* src = a.mid_o + row * DV + d0 + lane * 8;
-        acc0 += w * *reinterpret_cast<const f32x4*>(src);
-        acc1 += w * *reinterpret_cast<const f32x4*>(src + 4);
+    for (int s0 = 0; s0 < count; s0 += BATCH) {
+      float w[BATCH];
+      i16x8 v[BATCH];
+#pragma unroll
+      for (int j = 0; j < BATCH; ++j) {
+        const int s = s0 + j;
+        const int64_t row = (int64_t)(slot0 + min(s, count - 1)) * a.num_heads + head;
+        w[j] = s < count ? fast_exp2(a.mid_lse[row] - m) : 0.0f;
+        // rows past `count` repeat the last written row with weight 0
+        v[j] = *reinterpret_cast<const i16x8*>(a.mid_o + row * DV + d0 + lane * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < BATCH; ++j) {
+        wsum += w[j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += w[j] * Elt<DT>::to_float(v[j][e]);
       }
     }
     const float inv = wsum > 0.0f ? 1.0f / wsum : 1.0f;
-    i16x8 v;
+    i16x8 o;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = Elt<DT>::from_float(acc0[e] * inv);
-      v[4 + e] = Elt<DT>::from_float(acc1[e] * inv);
-    }
-    *reinterpret_cast<i16x8*>(orow + d0 + lane * 8) = v;
+    for (int e = 0; e < 8; ++e) o[e] = Elt<DT>::from_float(acc[e] * inv);
+    *reinterpret_cast<i16x8*>(orow + d0 + lane * 8) = o;
     if (d0 == 0 && lane == 0)
       a.lse[(int64_t)b * a.num_heads + head] = wsum > 0.0f ? (m + fast_log2(wsum)) * kLn2 : -INFINITY;
   }
@@ -798,7 +1014,7 @@ int hip_fail(hipError_t e, const char* where) {
 size_t workspace_bytes(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
   if (batch < 0 || heads < 0 || dv < 0) return 0;
   const int64_t slots = splits > 0 ? (int64_t)batch * splits : (int64_t)workers + batch;
-  const size_t o = (size_t)slots * heads * dv * sizeof(float);
+  const size_t o = (size_t)slots * heads * dv * 2;  // partials in the input dtype
   const size_t l = (size_t)slots * heads * sizeof(float);
   return ((o + 255) & ~(size_t)255) + l;
 }
@@ -848,7 +1064,7 @@ extern "C" {
 
 const char* tmla_last_error(void) { return g_err; }
 
-int tmla_version(void) { return 100; }
+int tmla_version(void) { return 101; }
 
 size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v, int32_t num_splits,
                             int32_t num_workers) {
@@ -909,8 +1125,8 @@ int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_
   a.lse = lse;
   char* ws = static_cast<char*>(workspace);
   const int64_t slots = num_splits > 0 ? (int64_t)batch * num_splits : (int64_t)num_workers + batch;
-  a.mid_o = reinterpret_cast<float*>(ws);
-  a.mid_lse = reinterpret_cast<float*>(ws + (((size_t)slots * num_heads * 512 * 4 + 255) & ~(size_t)255));
+  a.mid_o = reinterpret_cast<short*>(ws);
+  a.mid_lse = reinterpret_cast<float*>(ws + (((size_t)slots * num_heads * 512 * 2 + 255) & ~(size_t)255));
 
   const int nw = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
   const int heads_per_wg = 32 * nw;
@@ -946,8 +1162,8 @@ int tmla_mla_decode_combine(const int32_t* seqlens, int32_t batch, int32_t num_h
   a.lse = lse;
   const char* ws = static_cast<const char*>(workspace);
   const int64_t slots = num_splits > 0 ? (int64_t)batch * num_splits : (int64_t)num_workers + batch;
-  a.mid_o = reinterpret_cast<const float*>(ws);
-  a.mid_lse = reinterpret_cast<const float*>(ws + (((size_t)slots * num_heads * 512 * 4 + 255) & ~(size_t)255));
+  a.mid_o = reinterpret_cast<const short*>(ws);
+  a.mid_lse = reinterpret_cast<const float*>(ws + (((size_t)slots * num_heads * 512 * 2 + 255) & ~(size_t)255));
   dim3 grid(batch, (num_heads + 3) / 4);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TMLA_BF16)
