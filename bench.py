@@ -6,8 +6,13 @@ A step is one mla_decode (split-KV partial kernel + log-sum-exp combine) over
 the measured workload: batch 32, 128 heads, 8192 cached tokens per sequence,
 bf16, page size 64, shuffled block tables, inputs ~ N(0, 1) drawn on the CPU
 with seed 0 and resident in HBM before timing. Every step is preceded by a
-512 MiB write that evicts the 256 MiB Infinity Cache; HIP events on the
+512 MiB read that evicts the 256 MiB Infinity Cache (a read, so no dirty
+lines are left for the timed kernels to write back); HIP events on the
 launch stream bracket each kernel.
+
+``--copy-mib N`` adds, after the timed steps, three device-to-device copies
+of N MiB: kernels of known traffic against which the HBM counters of a
+profiler run (FETCH_SIZE, WRITE_SIZE) are scaled.
 
 Prints one JSON line: throughput in TFLOP/s (flops = 2 * H * (576 + 512) per
 cached token), microseconds per step, the HBM roofline of the dominant
@@ -43,6 +48,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-oracle sample time")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-flush", action="store_true", help="do not evict caches between steps")
+    p.add_argument("--copy-mib", type=int, default=0,
+                   help="after timing, run 3 copies of this many MiB (counter calibration)")
     return p.parse_args()
 
 
@@ -102,7 +109,9 @@ def main():
         call.combine()
     torch.cuda.synchronize(dev)
 
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    # timed region: each step is partial + combine between two events on the
+    # launch stream (no event between the kernels, which would add a gap)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
     torch.cuda.synchronize(dev)
     wall0 = time.perf_counter()
     for i in range(args.steps):
@@ -110,15 +119,58 @@ def main():
             flush()
         ev[i][0].record(stream)
         call.partial()
-        ev[i][1].record(stream)
         call.combine()
-        ev[i][2].record(stream)
+        ev[i][1].record(stream)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - wall0
 
-    step_us = [e[0].elapsed_time(e[2]) * 1e3 for e in ev]
-    partial_us = [e[0].elapsed_time(e[1]) * 1e3 for e in ev]
-    combine_us = [e[1].elapsed_time(e[2]) * 1e3 for e in ev]
+    # the dominant kernel alone, same number of launches, for the roofline
+    evp = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        if flush:
+            flush()
+        evp[i][0].record(stream)
+        call.partial()
+        evp[i][1].record(stream)
+    torch.cuda.synchronize(dev)
+
+    # the same step captured once in a HIP graph and replayed (how a serving
+    # loop launches it); every replay must reproduce the eager result exactly
+    graph_us = None
+    eager_out = call.out.clone()
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            call.partial()
+            call.combine()
+        evg = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+        for i in range(args.steps):
+            if flush:
+                flush()
+            evg[i][0].record(stream)
+            graph.replay()
+            evg[i][1].record(stream)
+        torch.cuda.synchronize(dev)
+        if torch.equal(call.out, eager_out):
+            graph_us = statistics.median([e[0].elapsed_time(e[1]) * 1e3 for e in evg])
+        else:
+            print("graph replay differs from the eager step; graph timing not reported", file=sys.stderr)
+        del graph
+    except RuntimeError as exc:  # capture unsupported in this environment
+        print(f"graph capture failed: {exc}", file=sys.stderr)
+
+    if args.copy_mib > 0:
+        src = torch.ones(args.copy_mib << 18, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            if flush:
+                flush()
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        del src, dst
+
+    step_us = [e[0].elapsed_time(e[1]) * 1e3 for e in ev]
+    partial_us = [e[0].elapsed_time(e[1]) * 1e3 for e in evp]
     us = statistics.median(step_us)
     p_us = statistics.fmean(partial_us)
 
@@ -149,10 +201,11 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "mla_partial_kernel", "achieved": round(achieved_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "algorithmic_bytes": nbytes,
-                     "partial_us_mean": round(p_us, 2), "combine_us_mean": round(statistics.fmean(combine_us), 2),
+                     "partial_us_mean": round(p_us, 2), "step_us_mean": round(statistics.fmean(step_us), 2),
                      "step_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
         "wall_s_timed_region": round(wall, 4),
+        "us_per_step_graph": None if graph_us is None else round(graph_us, 2),
     }
 
     if not args.no_cpu_baseline:

@@ -1,0 +1,155 @@
+"""triton-mla-bench: time mla_decode against PyTorch eager and torch.compile.
+
+    triton-mla-bench --batch 1 32 128 --seqlen 1024 4096 16384
+    python -m triton_mla.bench --workload b32_h128_ctx8k ragged_b64_h16_ctx1k-32k
+
+Same command line and CSV columns as the reference's benchmark
+(src/triton_mla/bench.py:16-108): --batch/--seqlen grid, --heads,
+--page-size, --dtype, --compile-mode, --no-eager, --csv. The ``triton_us``
+column keeps its name for drop-in CSV consumers and holds the HIP kernels'
+time; ``config`` names the launch shape that ran. Additions: --workload runs
+the named seeded workloads of triton_mla.workloads (uniform and ragged
+lengths), --splits picks the split scheme, --no-compile skips torch.compile.
+
+Timing: median of --reps runs, each preceded by a 512 MiB read that evicts
+the Infinity Cache, bracketed by HIP events on the current stream (the
+reference uses triton.testing.do_bench with a 256 MiB flush). Bytes and FLOPs
+follow the reference's formulas (src/triton_mla/bench.py:80-81) with the sum
+of sequence lengths for ragged batches.
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import os
+
+import torch
+
+from . import workloads
+from .kernel import DecodeLaunch, _num_sms
+from .reference import mla_decode_torch
+from .timing import Flusher, time_us
+
+DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16}
+CSV_FIELDS = ["gpu", "batch", "seqlen", "heads", "num_splits", "config", "bytes", "triton_us", "eager_us", "compile_us"]
+WORKLOADS = {
+    "b1_h128_ctx1k": workloads.b1_h128_1k,
+    "b8_h128_ctx1k": workloads.b8_h128_1k,
+    "b32_h128_ctx8k": workloads.b32_h128_8k,
+    "ragged_b64_h128_ctx1k-32k": workloads.ragged_b64_h128,
+    "ragged_b64_h16_ctx1k-32k": workloads.ragged_b64_h16,
+}
+
+
+def make_inputs(batch, seqlen, num_heads, page_size, dtype, device, seed=0):
+    """Uniform-length inputs (the reference's make_inputs recipe, seeded)."""
+    inp = workloads.uniform(batch, num_heads, seqlen, dtype=dtype, seed=seed, page=page_size)
+    return inp.to(device)
+
+
+def _splits_arg(text):
+    return None if text == "balanced" else int(text)
+
+
+def bench_one(inp, args, device, flush, compiled, writer, gpu):
+    splits = _splits_arg(args.splits)
+    call = DecodeLaunch(inp.q, inp.kv_cache, inp.seqlens, inp.block_table, 512, inp.softmax_scale, splits)
+    call.run()
+    torch.cuda.synchronize(device)
+    out = call.out
+
+    def run_torch(fn):
+        return fn(inp.q, inp.kv_cache, inp.seqlens, inp.block_table, softmax_scale=inp.softmax_scale)
+
+    t_compile = None
+    if compiled is not None:
+        ref = run_torch(compiled)
+        torch.testing.assert_close(out.float(), ref.float(), atol=2e-2, rtol=2e-2)
+        t_compile = time_us(lambda: run_torch(compiled), reps=args.reps, flush=flush, device=device)["median"]
+    elif not args.no_eager:
+        ref = run_torch(mla_decode_torch)
+        torch.testing.assert_close(out.float(), ref.float(), atol=2e-2, rtol=2e-2)
+
+    t_hip = time_us(call.run, reps=args.reps, flush=flush, device=device)["median"]
+    t_eager = None
+    if not args.no_eager:
+        t_eager = time_us(lambda: run_torch(mla_decode_torch), reps=max(args.reps // 4, 5), flush=flush,
+                          device=device)["median"]
+
+    nbytes = inp.algorithmic_bytes()
+    flops = inp.flops()
+    workers = call.workers or call.splits * inp.batch
+    config = f"hip/w{min(4, max(1, -(-inp.heads // 32)))}/" + (
+        f"balanced{workers}" if splits is None else f"splits{splits}")
+    seqlen = int(inp.seqlens.max())
+    row = [inp.batch, seqlen, args.splits, config, f"{t_hip:.1f}", f"{nbytes / t_hip / 1e6:.2f}",
+           f"{flops / t_hip / 1e6:.0f}"]
+    if not args.no_eager:
+        row.append(f"{t_eager:.1f}")
+    if t_compile is not None:
+        row += [f"{t_compile:.1f}", f"{t_compile / t_hip:.2f}x"]
+    print("| " + " | ".join(str(c) for c in row) + " |", flush=True)
+    if writer:
+        writer.writerow({"gpu": gpu, "batch": inp.batch, "seqlen": seqlen, "heads": inp.heads,
+                         "num_splits": args.splits, "config": config, "bytes": nbytes, "triton_us": t_hip,
+                         "eager_us": t_eager, "compile_us": t_compile})
+
+
+def main(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    parser.add_argument("--batch", type=int, nargs="+", default=[1, 8, 32, 64, 128])
+    parser.add_argument("--seqlen", type=int, nargs="+", default=[1024, 4096, 8192, 16384, 32768])
+    parser.add_argument("--heads", type=int, default=128, help="128 for one GPU, 16 per GPU under TP8")
+    parser.add_argument("--page-size", type=int, default=64)
+    parser.add_argument("--dtype", choices=DTYPES, default="bf16")
+    parser.add_argument("--compile-mode", default="max-autotune-no-cudagraphs")
+    parser.add_argument("--no-eager", action="store_true")
+    parser.add_argument("--no-compile", action="store_true", help="skip the torch.compile baseline")
+    parser.add_argument("--csv", help="also write results to this CSV file")
+    parser.add_argument("--workload", nargs="+", choices=sorted(WORKLOADS),
+                        help="run these named workloads instead of the --batch x --seqlen grid")
+    parser.add_argument("--splits", default="balanced", help="'balanced' or a per-sequence split count")
+    parser.add_argument("--reps", type=int, default=100)
+    args = parser.parse_args(argv)
+
+    device = torch.device("cuda")
+    dtype = DTYPES[args.dtype]
+    flush = Flusher(device)
+    compiled = None
+    if not args.no_compile:
+        compiled = torch.compile(mla_decode_torch, mode=args.compile_mode, dynamic=False)
+
+    gpu = torch.cuda.get_device_name()
+    writer = None
+    if args.csv:
+        os.makedirs(os.path.dirname(os.path.abspath(args.csv)), exist_ok=True)
+        csv_file = open(args.csv, "w", newline="")
+        writer = csv.DictWriter(csv_file, fieldnames=CSV_FIELDS)
+        writer.writeheader()
+
+    print(f"# {gpu}  CUs={_num_sms(device)}  heads={args.heads}  page={args.page_size}  {args.dtype}")
+    cols = ["batch", "seqlen", "splits", "config", "hip us", "TB/s", "TFLOPS"]
+    if not args.no_eager:
+        cols.append("eager us")
+    if compiled is not None:
+        cols += ["compile us", "speedup"]
+    print("| " + " | ".join(cols) + " |")
+    print("|" + "---|" * len(cols))
+
+    if args.workload:
+        cases = [lambda name=name: WORKLOADS[name](dtype).to(device) for name in args.workload]
+    else:
+        cases = [lambda b=b, s=s: make_inputs(b, s, args.heads, args.page_size, dtype, device)
+                 for b in args.batch for s in args.seqlen]
+    for make in cases:
+        inp = make()
+        bench_one(inp, args, device, flush, compiled, writer, gpu)
+        del inp
+        torch.cuda.empty_cache()
+    if writer:
+        csv_file.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -16,13 +16,17 @@ import torch
 
 
 class Flusher:
+    """A row-sum over ``flush_bytes`` of int64: one reduction kernel that reads
+    the whole buffer and writes 8 KiB (same dtype in and out, so no converted
+    copy of the buffer is materialised)."""
+
     def __init__(self, device, flush_bytes: int = 512 << 20):
         rows = 1024
-        self.buf = torch.ones(rows, max(flush_bytes // 4 // rows, 1), dtype=torch.int32, device=device)
+        self.buf = torch.ones(rows, max(flush_bytes // 8 // rows, 1), dtype=torch.int64, device=device)
         self.sink = torch.empty(rows, dtype=torch.int64, device=device)
 
     def __call__(self):
-        torch.sum(self.buf, dim=1, dtype=torch.int64, out=self.sink)
+        torch.sum(self.buf, dim=1, out=self.sink)
 
 
 def time_us(fn, reps: int = 100, warmup: int = 5, flush: Flusher | None = None,
