@@ -42,7 +42,7 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--splits", default="balanced",
                    help="'balanced' (device-side tile balancing) or an integer split count")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-oracle sample time")
@@ -135,26 +135,20 @@ def main():
     torch.cuda.synchronize(dev)
 
     # the same step captured once in a HIP graph and replayed (how a serving
-    # loop launches it); every replay must reproduce the eager result exactly
-    graph_us = None
+    # loop launches it): every replay must reproduce the eager result exactly
     eager_out = call.out.clone()
+    graph_ok = None
     try:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             call.partial()
             call.combine()
-        evg = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
-        for i in range(args.steps):
-            if flush:
-                flush()
-            evg[i][0].record(stream)
+        graph_ok = True
+        for _ in range(3):
+            call.out.zero_()
             graph.replay()
-            evg[i][1].record(stream)
-        torch.cuda.synchronize(dev)
-        if torch.equal(call.out, eager_out):
-            graph_us = statistics.median([e[0].elapsed_time(e[1]) * 1e3 for e in evg])
-        else:
-            print("graph replay differs from the eager step; graph timing not reported", file=sys.stderr)
+            torch.cuda.synchronize(dev)
+            graph_ok = graph_ok and torch.equal(call.out, eager_out)
         del graph
     except RuntimeError as exc:  # capture unsupported in this environment
         print(f"graph capture failed: {exc}", file=sys.stderr)
@@ -205,7 +199,7 @@ def main():
                      "step_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
         "wall_s_timed_region": round(wall, 4),
-        "us_per_step_graph": None if graph_us is None else round(graph_us, 2),
+        "graph_replay_matches_eager": graph_ok,
     }
 
     if not args.no_cpu_baseline:

@@ -111,8 +111,11 @@ __device__ __forceinline__ void pin_vgpr(f32x16& x) { asm volatile("" : "+v"(x))
 __device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x)); }
 // (Operand-constrained asm lives in __device__ helpers only: the host pass
 // of the compiler rejects GPU register constraints inside a kernel body.)
+__device__ __forceinline__ void pin_f1(float& a) { asm volatile("" : "+v"(a)); }
 __device__ __forceinline__ void pin_f2(float& a, float& b) { asm volatile("" : "+v"(a), "+v"(b)); }
 __device__ __forceinline__ void pin_f3(float& a, float& b, float& c) { asm volatile("" : "+v"(a), "+v"(b), "+v"(c)); }
+__device__ __forceinline__ void pin_f4(f32x4& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin_f16(f32x16& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin_f8(float* x) {
   asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]));
 }
@@ -187,14 +190,14 @@ __device__ __forceinline__ void lgkm_tie(i16x8& k, i16x4& vl, i16x4& vh, i16x8& 
     asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(p) : "i"(N));
 }
 
-// LDS reads issued by fetch(t) of a pass (one K operand per S step; two V^T
-// halves at the first head block of a PV column block, one P^T operand at the
-// first column block of a (token half, head block)).
-template <int NS, int NV, int PV0, int NW>
+// LDS reads issued by fetch(t) of a pass (one K operand per S step; from step
+// PVOFF on, two V^T halves at the first head block of a PV column block and
+// one P^T operand at the first column block of a (token half, head block)).
+template <int NS, int NV, int PV0, int NW, int PVOFF>
 constexpr int pass_reads(int t) {
   int n = t < NS ? 1 : 0;
-  if (t < NV) {
-    const int g = PV0 + t;
+  if (t >= PVOFF && t - PVOFF < NV) {
+    const int g = PV0 + t - PVOFF;
     n += (g % NW == 0 ? 2 : 0) + ((g % 16) / NW == 0 ? 1 : 0);
   }
   return n;
@@ -238,10 +241,21 @@ __device__ __forceinline__ void mfma_vgpr_fence(f32x16& d) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(d));
 }
 
-// One LDS-DMA copy: 16 bytes per lane from `src` into LDS at dst + 16 * lane
-// (global_load_lds_dwordx4; completion counts in vmcnt).
+// 16-byte store written through to memory (sc0 sc1: system-scope write-
+// through), so a kernel that ends with many such stores leaves no dirty L2
+// lines for the end-of-kernel write-back.
+__device__ __forceinline__ void store_through(i16x8* p, i16x8 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" : : "v"(p), "v"(v) : "memory");
+}
+
+// One LDS-DMA copy: 16 bytes per lane from src + OFF into LDS at
+// dst + 16 * lane (global_load_lds_dwordx4; completion counts in vmcnt). The
+// instruction's immediate offset applies to both addresses, so the LDS base
+// (M0, a scalar) is lowered by OFF and the per-lane address needs no add.
+template <int OFF>
 __device__ __forceinline__ void lds_copy16(const char* src, char LDS_AS* dst) {
-  __builtin_amdgcn_global_load_lds(src, (void LDS_AS*)dst, 16, 0, 0);
+  static_assert(OFF >= 0 && OFF < 4096, "immediate offset range");
+  __builtin_amdgcn_global_load_lds(src, (void LDS_AS*)(dst - OFF), 16, OFF, 0);
 }
 
 // Workgroup barrier that the compiler treats as a full memory-ordering point
@@ -551,41 +565,44 @@ void mla_partial_kernel(PartialArgs a) {
         src[ri] = a.kv + row_offset<PAGED>(a, b, tok, n_b, pg) + ((lane & 7) ^ piece_swizzle(dma_r, rg)) * 16;
       }
     };
-    auto copy_one = [&](int st, int ri, int cb, const char* const (&src)[RG_PER_WAVE]) __attribute__((always_inline)) {
+    auto copy_one = [&](int st, int ri, auto CB, const char* const (&src)[RG_PER_WAVE]) __attribute__((always_inline)) {
+      constexpr int cb = decltype(CB)::value;
       const int rg = wave * RG_PER_WAVE + ri;
       char LDS_AS* dst = cb < NVB ? lds + (st - st0) % kStages * VSLOT + (rg * NVB + cb) * 1024
                                   : lds + OFF_R + (st - st0) % kRopeStages * RSLOT + (rg * NRB + cb - NVB) * 1024;
-      lds_copy16(src[ri] + cb * 128, dst);
+      lds_copy16<cb * 128>(src[ri], dst);
     };
     auto issue = [&](int st, int page) __attribute__((always_inline)) {
       const char* src[RG_PER_WAVE];
       copy_src(st, page, src);
 #pragma unroll
       for (int ri = 0; ri < RG_PER_WAVE; ++ri)
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) copy_one(st, ri, cb, src);
+        static_for<NCB>([&](auto CB) __attribute__((always_inline)) { copy_one(st, ri, CB, src); });
     };
 
     // One pass over a sub-tile pair: S^T of the sub-tile in kst (DO_S) and
-    // PV steps [PV0, PV1) of O^T += V^T P^T for the sub-tile in vst,
-    // interleaved step by step so the MFMA pipe alternates between the
-    // independent S chain and the PV accumulators. PV step g is MFMA
-    // (c, j4, hb) = (g / 16, (g % 16) / NW, g % NW); its V^T operand is read
-    // at the first hb of each j4 and its P^T operand at the first j4 of each
-    // c. LDS operands run PD steps ahead; each step waits with an lgkmcnt
-    // that counts exactly the reads issued after its own. hook(step) runs
-    // after each step's MFMAs (copies of a later sub-tile, softmax pieces),
-    // so its VALU and memory work overlaps them.
+    // PV steps [PV0, PV1) of O^T += V^T P^T for the sub-tile in vst, the
+    // latter starting at step PVOFF, interleaved step by step so the MFMA
+    // pipe alternates between the independent S chain and the PV
+    // accumulators. PV step g is MFMA (c, j4, hb) = (g / 16, (g % 16) / NW,
+    // g % NW); its V^T operand is read at the first hb of each j4 and its P^T
+    // operand at the first j4 of each c. LDS operands run PD steps ahead;
+    // each step waits with an lgkmcnt that counts exactly the reads issued
+    // after its own. hook(step) runs after each step's MFMAs (copies of a
+    // later sub-tile, the rescale check, softmax pieces), so its VALU and
+    // memory work overlaps them.
     constexpr int PD = 2;
     constexpr int PV_SPLIT = 16;  // PV steps beside S; the rest beside the softmax
+    constexpr int PV_START = 4;   // S-only steps first: the rescale factors arrive meanwhile
     static_assert(PV_SPLIT % NW == 0 && PV_SPLIT >= 16, "a V^T operand never spans the two passes");
-    auto pass = [&](auto DOS, auto PVLO, auto PVHI, const char LDS_AS* kst_v, const char LDS_AS* kst_r,
+    auto pass = [&](auto DOS, auto PVLO, auto PVHI, auto PVOFFC, const char LDS_AS* kst_v, const char LDS_AS* kst_r,
                     const char LDS_AS* vst, const char LDS_AS* pst, f32x16& s, auto&& hook)
                     __attribute__((always_inline)) {
       constexpr bool do_s = decltype(DOS)::value;
       constexpr int PV0 = decltype(PVLO)::value;
+      constexpr int PVOFF = decltype(PVOFFC)::value;
       constexpr int NS = do_s ? NKC : 0, NV = decltype(PVHI)::value - PV0;
-      constexpr int NSTEPS = NS > NV ? NS : NV;
+      constexpr int NSTEPS = NS > NV + PVOFF ? NS : NV + PVOFF;
       const char LDS_AS* kvb[4] = {kst_v + k_off_v[0], kst_v + k_off_v[1], kst_v + k_off_v[2], kst_v + k_off_v[3]};
       const char LDS_AS* krb[4] = {kst_r + k_off_r[0], kst_r + k_off_r[1], kst_r + k_off_r[2], kst_r + k_off_r[3]};
       const char LDS_AS* vbase[2][2] = {{vst + v_off[0][0], vst + v_off[0][1]},
@@ -602,8 +619,8 @@ void mla_partial_kernel(PartialArgs a) {
           else
             kb[t % (PD + 1)] = ds_read_b128<(cb - NVB) * 1024>(krb[t & 3]);
         }
-        if constexpr (t < NV) {
-          constexpr int g = PV0 + t, c = g / 16, j4 = (g % 16) / NW, hb = g % NW;
+        if constexpr (t >= PVOFF && t - PVOFF < NV) {
+          constexpr int g = PV0 + t - PVOFF, c = g / 16, j4 = (g % 16) / NW, hb = g % NW;
           if constexpr (hb == 0) {
             constexpr int off = c * 2 * NVB * 1024 + (j4 >> 1) * 1024;
             vl[c * NDBW + j4] = ds_read_tr<off>(vbase[j4 & 1][0]);
@@ -620,13 +637,14 @@ void mla_partial_kernel(PartialArgs a) {
         constexpr int last = (j + PD < NSTEPS - 1) ? j + PD : NSTEPS - 1;
         constexpr int after = [] {
           int n = 0;
-          for (int t = j + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NW>(t);
+          for (int t = j + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NW, PVOFF>(t);
           return n;
         }();
-        constexpr int g = PV0 + (j < NV ? j : 0), c = g / 16, j4 = (g % 16) / NW, hb = g % NW;
+        constexpr bool pv = j >= PVOFF && j - PVOFF < NV;
+        constexpr int g = PV0 + (pv ? j - PVOFF : 0), c = g / 16, j4 = (g % 16) / NW, hb = g % NW;
         constexpr bool has_k = j < NS;
-        constexpr bool has_v = j < NV && hb == 0;
-        constexpr bool has_p = j < NV && j4 == 0;
+        constexpr bool has_v = pv && hb == 0;
+        constexpr bool has_p = pv && j4 == 0;
         constexpr int vi = c * NDBW + j4;
         constexpr int r = j % (PD + 1);
         // the wait ties the operands read for this step to it (a step that
@@ -639,7 +657,7 @@ void mla_partial_kernel(PartialArgs a) {
           else
             mfma_vgpr_acc<DT>(s, kb[r], qop[j]);
         }
-        if constexpr (j < NV) {
+        if constexpr (pv) {
           const i16x4 lo = vl[vi], hi4 = vh[vi];
           const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
           acc[j4 * NW + hb] = Elt<DT>::mfma(vop, pop[c][hb], acc[j4 * NW + hb]);
@@ -736,67 +754,76 @@ void mla_partial_kernel(PartialArgs a) {
       // with the ring entries refilled during this iteration
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       lds_barrier();
+      // the page-id load goes out before every LDS read of the iteration, so
+      // its out-of-order return can only make the counted waits wait longer
+      if (PAGED && PAGE_UNIFORM && i >= 0 && i + kStages < nst) next_page = page_fetch(st0 + i + kStages);
       const int pbuf = i & 1;
       f32x4 alpha4 = ds_read_f32x4(lds + OFF_A + pbuf * ASLOT + (lane & 31) * 16);
-      const char* csrc[RG_PER_WAVE];
-      if (do_copy) copy_src(st0 + i + kStages - 1, page, csrc);
-      lgkm_tie_f4<0>(alpha4);
-      // issued after the last counted LDS wait before the passes, so its
-      // out-of-order return can only make later waits wait longer
-      if (PAGED && PAGE_UNIFORM && i >= 0 && i + kStages < nst) next_page = page_fetch(st0 + i + kStages);
-      {
-        bool any = false;
-#pragma unroll
-        for (int hb = 0; hb < NW; ++hb) any |= alpha4[hb] != 1.0f;
-        if (__builtin_amdgcn_ballot_w64(any) != 0) rescale(alpha4);
-      }
       const char LDS_AS* vst = lds + (i < 0 ? 0 : i % kStages) * VSLOT;
       const char LDS_AS* kst_v = lds + (i + 1) % kStages * VSLOT;
       const char LDS_AS* kst_r = lds + (i + 1) % kRopeStages * RSLOT;
       const char LDS_AS* pst = lds + OFF_P + pbuf * PSLOT;
       const int st_s = st0 + i + 1;  // sub-tile of this iteration's S
 
-      // pass 1: S(i+1) and PV(i) steps [0, PV_SPLIT), with the copies of
-      // sub-tile i+3 spread over the S steps
-      auto copy_hook = [&](auto J) __attribute__((always_inline)) {
+      // pass 1: S(i+1) and PV(i) steps [0, PV_SPLIT) from step PV_START on;
+      // the copies of sub-tile i+3 are spread over the S steps, and the
+      // factors published for PV(i) are applied before its first MFMA (the
+      // wait of step PV_START - 1 covers their read, which is older than
+      // every read of the pass)
+      const char* csrc[RG_PER_WAVE];
+      auto pass1_hook = [&](auto J) __attribute__((always_inline)) {
         constexpr int j = decltype(J)::value;
+        if constexpr (j == 0) {
+          if (do_copy) copy_src(st0 + i + kStages - 1, page, csrc);
+        }
+        if constexpr (j == PV_START - 1) {
+          pin_f4(alpha4);
+          bool any = false;
+#pragma unroll
+          for (int hb = 0; hb < NW; ++hb) any |= alpha4[hb] != 1.0f;
+          if (__builtin_amdgcn_ballot_w64(any) != 0) rescale(alpha4);
+        }
         if constexpr (j % COPY_STRIDE == COPY_STRIDE / 2 && j / COPY_STRIDE < LOADS) {
           constexpr int idx = j / COPY_STRIDE;
-          if (do_copy) copy_one(st0 + i + kStages - 1, idx / NCB, idx % NCB, csrc);
+          if (do_copy) copy_one(st0 + i + kStages - 1, idx / NCB, std::integral_constant<int, idx % NCB>{}, csrc);
         }
       };
       f32x16 s;
-      pass(std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{}, kst_v, kst_r,
-           vst, pst, s, copy_hook);
+      pass(std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
+           std::integral_constant<int, PV_START>{}, kst_v, kst_r, vst, pst, s, pass1_hook);
 
       // pass 2: PV(i) steps [PV_SPLIT, 2 * NDB) beside the softmax of
       // sub-tile i+1 (heads of this wave), base-2 with the lazy rescale: the
       // reference max only moves, for the whole wave, when a score exceeds
       // it by 2^kRescaleLog2 (then both token halves of every head agree on
-      // the new max through one lane exchange).
+      // the new max through one lane exchange). Scores stay unscaled: the
+      // max is taken on s (scale > 0) or -s (scale < 0) and the scale is
+      // folded into p = 2^(s * c - m).
       const bool full = (st_s + 1) * kSubTokens <= n_b;  // no token past the sequence
-      float x[16];
+      const float c = a.qk_scale_log2;
       float m_use = m_run, lsum = 0.0f, alpha = 1.0f;
       i16x8 pnext[2];
       auto softmax_hook = [&](auto J) __attribute__((always_inline)) {
         constexpr int j = decltype(J)::value;
-        if constexpr (j < 2) {  // scale (and mask) 8 scores
-          if (full) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) x[8 * j + e] = s[8 * j + e] * a.qk_scale_log2;
-          } else {
+        if constexpr (j == 0) {  // mask tokens past the sequence (last sub-tile only)
+          if (!full) {
             const int tok0 = st_s * kSubTokens + 4 * hi;
+            const float off = c >= 0.0f ? -INFINITY : INFINITY;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int r = 8 * j + e;
-              x[r] = tok0 + 8 * (r >> 2) + (r & 3) < n_b ? s[r] * a.qk_scale_log2 : -INFINITY;
-            }
+            for (int r = 0; r < 16; ++r)
+              if (tok0 + 8 * (r >> 2) + (r & 3) >= n_b) s[r] = off;
           }
-          pin_f8(&x[8 * j]);
-        } else if constexpr (j == 2) {  // reference max
-          float mx = x[0];
+          pin_f16(s);
+        } else if constexpr (j == 1) {  // reference max
+          float mx = c >= 0.0f ? s[0] : -s[0];
+          if (c >= 0.0f) {
 #pragma unroll
-          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, x[r]);
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+          } else {
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, -s[r]);
+          }
+          mx *= fabsf(c);
           if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleLog2) != 0) {
             // the exchange is an LDS operation outside the pass's
             // counting: let every counted read finish first
@@ -805,21 +832,22 @@ void mla_partial_kernel(PartialArgs a) {
             if (m_run != -INFINITY) alpha = fast_exp2(m_run - m_use);
           }
           pin_f2(m_use, alpha);
-        } else if constexpr (j >= 3 && j < 11) {  // two probabilities
+        } else if constexpr (j >= 2 && j < 10) {  // two probabilities
 #pragma unroll
           for (int e = 0; e < 2; ++e) {
-            const int r = 2 * (j - 3) + e;
-            x[r] = fast_exp2(x[r] - m_use);
-            lsum += x[r];
+            const int r = 2 * (j - 2) + e;
+            s[r] = fast_exp2(fmaf(s[r], c, -m_use));  // masked: +-inf * c = -inf -> 0
+            lsum += s[r];
           }
-          pin_f3(x[2 * (j - 3)], x[2 * (j - 3) + 1], lsum);
-        } else if constexpr (j == 11) {
+          pin_f16(s);
+          pin_f1(lsum);
+        } else if constexpr (j == 10) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) pnext[r >> 3][r & 7] = Elt<DT>::from_float(x[r]);
+          for (int r = 0; r < 16; ++r) pnext[r >> 3][r & 7] = Elt<DT>::from_float(s[r]);
         }
       };
-      pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * NDB>{}, kst_v,
-           kst_r, vst, pst, s, softmax_hook);
+      pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * NDB>{},
+           std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s, softmax_hook);
       {
         char LDS_AS* pw = lds + OFF_P + (pbuf ^ 1) * PSLOT + wave * 2 * 1024 + lane * 16;
         ds_write_b128<0>(pw, pnext[0]);
@@ -879,8 +907,8 @@ void mla_partial_kernel(PartialArgs a) {
 #pragma unroll
       for (int r = 0; r < 32; ++r)
         if (r < rows)
-          *reinterpret_cast<i16x8*>(dst + r * row_stride + lane * 8) =
-              *reinterpret_cast<const i16x8 LDS_AS*>(obuf + r * OPITCH + lane * 16);
+          store_through(reinterpret_cast<i16x8*>(dst + r * row_stride + lane * 8),
+                        *reinterpret_cast<const i16x8 LDS_AS*>(obuf + r * OPITCH + lane * 16));
       if (head_ok && hi == 0) {
         if (seg.direct)
           a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
@@ -954,29 +982,48 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
     if (lane == 0) a.lse[(int64_t)b * a.num_heads + head] = -INFINITY;
     return;
   }
-  // m = max over splits of lse2 (-inf -> 0)
-  float m = -INFINITY;
-  for (int s = lane; s < count; s += 64)
-    m = fmaxf(m, a.mid_lse[(int64_t)(slot0 + s) * a.num_heads + head]);
-  for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
-  if (m == -INFINITY) m = 0.0f;
-
-  // Eight partial rows in flight per batch: all loads of a batch are issued
-  // before any is consumed.
+  static_assert(DV == 512, "one row = 64 lanes x 8 elements");
+  // Up to BATCH splits (the common case): every lse and partial row is
+  // requested at once, then m = max lse2 (-inf -> 0), w = 2^(lse2 - m).
+  // Slots past `count` repeat the last written row with weight 0.
   constexpr int BATCH = 8;
-  for (int d0 = 0; d0 < DV; d0 += 512) {
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    float wsum = 0.0f;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float wsum = 0.0f, m = -INFINITY;
+  if (count <= BATCH) {
+    float l[BATCH];
+    i16x8 v[BATCH];
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      const int64_t row = (int64_t)(slot0 + min(j, count - 1)) * a.num_heads + head;
+      l[j] = a.mid_lse[row];
+      v[j] = *reinterpret_cast<const i16x8*>(a.mid_o + row * DV + lane * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j)
+      if (j < count) m = fmaxf(m, l[j]);
+    if (m == -INFINITY) m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      const float w = j < count ? fast_exp2(l[j] - m) : 0.0f;
+      wsum += w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += w * Elt<DT>::to_float(v[j][e]);
+    }
+  } else {
+    for (int s = lane; s < count; s += 64)
+      m = fmaxf(m, a.mid_lse[(int64_t)(slot0 + s) * a.num_heads + head]);
+    for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+    if (m == -INFINITY) m = 0.0f;
+    // eight partial rows in flight per batch
     for (int s0 = 0; s0 < count; s0 += BATCH) {
       float w[BATCH];
       i16x8 v[BATCH];
 #pragma unroll
       for (int j = 0; j < BATCH; ++j) {
-        const int s = s0 + j;
-        const int64_t row = (int64_t)(slot0 + min(s, count - 1)) * a.num_heads + head;
-        w[j] = s < count ? fast_exp2(a.mid_lse[row] - m) : 0.0f;
-        // rows past `count` repeat the last written row with weight 0
-        v[j] = *reinterpret_cast<const i16x8*>(a.mid_o + row * DV + d0 + lane * 8);
+        const int sj = s0 + j;
+        const int64_t row = (int64_t)(slot0 + min(sj, count - 1)) * a.num_heads + head;
+        w[j] = sj < count ? fast_exp2(a.mid_lse[row] - m) : 0.0f;
+        v[j] = *reinterpret_cast<const i16x8*>(a.mid_o + row * DV + lane * 8);
       }
 #pragma unroll
       for (int j = 0; j < BATCH; ++j) {
@@ -985,14 +1032,13 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
         for (int e = 0; e < 8; ++e) acc[e] += w[j] * Elt<DT>::to_float(v[j][e]);
       }
     }
-    const float inv = wsum > 0.0f ? 1.0f / wsum : 1.0f;
-    i16x8 o;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = Elt<DT>::from_float(acc[e] * inv);
-    *reinterpret_cast<i16x8*>(orow + d0 + lane * 8) = o;
-    if (d0 == 0 && lane == 0)
-      a.lse[(int64_t)b * a.num_heads + head] = wsum > 0.0f ? (m + fast_log2(wsum)) * kLn2 : -INFINITY;
   }
+  const float inv = wsum > 0.0f ? 1.0f / wsum : 1.0f;
+  i16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = Elt<DT>::from_float(acc[e] * inv);
+  *reinterpret_cast<i16x8*>(orow + lane * 8) = o;
+  if (lane == 0) a.lse[(int64_t)b * a.num_heads + head] = wsum > 0.0f ? (m + fast_log2(wsum)) * kLn2 : -INFINITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -1115,7 +1161,11 @@ int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_
   a.seqlens = seqlens;
   a.batch = batch;
   a.num_heads = num_heads;
+  // A zero scale (every score 0) runs as the smallest normal float instead:
+  // the probabilities then differ from 1 by far less than one ulp, and masked
+  // tokens (score -inf) still get exactly 0.
   a.qk_scale_log2 = softmax_scale * kLog2e;
+  if (a.qk_scale_log2 == 0.0f) a.qk_scale_log2 = 1.17549435e-38f;
   a.num_splits = num_splits;
   a.num_workers = num_workers;
   a.xcds = 8;  // MI355X: 8 XCDs
