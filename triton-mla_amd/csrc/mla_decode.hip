@@ -4,19 +4,20 @@
 // Reference behaviour: src/triton_mla/kernel.py (stage 1 kernel.py:43-138,
 // stage 2 kernel.py:141-181, host wrapper kernel.py:204-323).
 //
-// Design (one workgroup = one worker, 64 * NW threads, NW waves, 32 * NW heads):
+// Design (one workgroup = one worker, 4 waves = one per SIMD, 32 * NHB heads
+// with NHB = 1, 2 or 4 blocks of 32):
 //  * Each worker owns a range of 64-token tiles; it walks them as 32-token
 //    sub-tiles through LDS rings (V dims: 4 entries, rope dims: 3). Rows are
 //    copied HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging): one
 //    instruction moves eight full 128-byte lines into 1 KiB of LDS; the
 //    copies of sub-tile i+3 are spread over the MFMA steps of iteration i.
-//  * S^T = K . Q^T by head: wave w keeps Q^T of its 32 heads in VGPRs, reads
-//    K (all 576 dims) from LDS and runs the softmax of those heads.
-//  * O^T += V^T . P^T by value dimension: wave w owns DV/NW dims of every
-//    head of the workgroup (fp32 accumulators in AGPRs); P^T and the per-head
-//    rescale factors go through LDS, so each V^T operand (read straight from
-//    the row-major tile with ds_read_b64_tr_b16) feeds NW MFMAs.
-//    Both products run on v_mfma_f32_32x32x16_{bf16,f16}.
+//  * S^T = K . Q^T by head: wave w < NHB keeps Q^T of its 32 heads in VGPRs,
+//    reads K (all 576 dims) from LDS and runs the softmax of those heads.
+//  * O^T += V^T . P^T by value dimension: wave w owns 128 of the 512 dims of
+//    every head of the workgroup (fp32 accumulators in AGPRs); P^T and the
+//    per-head rescale factors go through LDS, so each V^T operand (read
+//    straight from the row-major tile with ds_read_b64_tr_b16) feeds NHB
+//    MFMAs. Both products run on v_mfma_f32_32x32x16_{bf16,f16}.
 //  * Online softmax in the base-2 domain with a lazy rescale: the running
 //    reference max only moves when a new score exceeds it by more than 2^8,
 //    so probabilities stay <= 256 and the O^T rescale is rare.
@@ -193,12 +194,12 @@ __device__ __forceinline__ void lgkm_tie(i16x8& k, i16x4& vl, i16x4& vh, i16x8& 
 // LDS reads issued by fetch(t) of a pass (one K operand per S step; from step
 // PVOFF on, two V^T halves at the first head block of a PV column block and
 // one P^T operand at the first column block of a (token half, head block)).
-template <int NS, int NV, int PV0, int NW, int PVOFF>
+template <int NS, int NV, int PV0, int NHB, int PVOFF>
 constexpr int pass_reads(int t) {
   int n = t < NS ? 1 : 0;
   if (t >= PVOFF && t - PVOFF < NV) {
     const int g = PV0 + t - PVOFF;
-    n += (g % NW == 0 ? 2 : 0) + ((g % 16) / NW == 0 ? 1 : 0);
+    n += (g % NHB == 0 ? 2 : 0) + ((g % (4 * NHB)) / NHB == 0 ? 1 : 0);
   }
   return n;
 }
@@ -341,14 +342,17 @@ struct Segment {
 // Block (rg, cb) holds rows 8rg..8rg+7, bytes [128cb, 128cb+128) of each row,
 // 16-byte piece p of row r at position r*8 + (p ^ piece_swizzle(r, rg)).
 //
-// Work split inside a workgroup of NW waves (32*NW heads):
-//  * S and the softmax by head: wave w owns heads 32w..32w+31 (its Q^T lives
-//    in its VGPRs) and writes their probabilities P^T and rescale factors to
-//    LDS;
-//  * O^T += V^T P^T by value dimension: wave w owns dims [w*DV/NW, (w+1)*DV/NW)
-//    of all 32*NW heads, so each V^T operand read from LDS feeds NW MFMAs.
-template <int DT, int DV, int DR, int NW, bool PAGED, bool PAGE_UNIFORM>
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(1, 1)))
+// Work split inside a workgroup of 4 waves (one per SIMD) and NHB blocks of
+// 32 heads (NHB = 1, 2, 4):
+//  * S and the softmax by head: wave w < NHB owns heads 32w..32w+31 (its Q^T
+//    lives in its VGPRs) and writes their probabilities P^T and rescale
+//    factors to LDS;
+//  * O^T += V^T P^T by value dimension: wave w owns dims [w*DV/4, (w+1)*DV/4)
+//    of all 32*NHB heads, so each V^T operand read from LDS feeds NHB MFMAs.
+// With fewer than 4 head blocks the waves past NHB only copy and run PV, so
+// small head counts still use every SIMD of the CU.
+template <int DT, int DV, int DR, int NHB, bool PAGED, bool PAGE_UNIFORM>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void mla_partial_kernel(PartialArgs a) {
   constexpr int DQK = DV + DR;
   static_assert(DQK % 64 == 0 && DV % 64 == 0, "row must be whole 128-byte blocks");
@@ -357,11 +361,13 @@ void mla_partial_kernel(PartialArgs a) {
   constexpr int NRB = NCB - NVB;          // ... and rope dims
   constexpr int NKC = DQK / 16;           // k-chunks of QK^T
   constexpr int NDB = DV / 32;            // 32-dim blocks of PV
+  constexpr int NW = 4;                   // waves per workgroup
   constexpr int NDBW = NDB / NW;          // ... owned by one wave
+  constexpr int NACC = NDBW * NHB;        // 32x32 accumulator blocks per wave
   constexpr int VSLOT = 4 * NVB * 1024;   // V ring entry
   constexpr int RSLOT = 4 * NRB * 1024;   // rope ring entry
   constexpr int kRopeStages = kStages - 1;
-  constexpr int PSLOT = NW * 2 * 1024;    // P^T of one sub-tile: [hb][c][lane] x 16 bytes
+  constexpr int PSLOT = NHB * 2 * 1024;   // P^T of one sub-tile: [hb][c][lane] x 16 bytes
   constexpr int ASLOT = 32 * 4 * 4;       // per-head factors: [head % 32][hb] floats
   constexpr int OFF_R = kStages * VSLOT;
   constexpr int OFF_P = OFF_R + kRopeStages * RSLOT;
@@ -370,10 +376,10 @@ void mla_partial_kernel(PartialArgs a) {
   constexpr int RG_PER_WAVE = 4 / NW;
   constexpr int LOADS = RG_PER_WAVE * NCB;  // DMA instructions per wave per sub-tile
   constexpr int OPITCH = DV * 2 + 16;        // output staging row pitch (bytes)
-  static_assert(NW == 1 || NW == 2 || NW == 4, "waves per workgroup");
+  static_assert(NHB == 1 || NHB == 2 || NHB == 4, "head blocks per workgroup");
   static_assert(NRB >= 1 && NDB % NW == 0 && NDBW % 2 == 0, "column split");
   static_assert(LOADS < 64, "vmcnt immediate range");
-  static_assert(NW * 32 * OPITCH <= OFF_P, "output staging fits the rings");
+  static_assert(NHB * 32 * OPITCH <= OFF_P, "output staging fits the rings");
   static_assert(DV == 512, "one output row = 64 lanes x 8 elements");
 
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
@@ -392,9 +398,10 @@ void mla_partial_kernel(PartialArgs a) {
   const int worker = (a.xcds > 1 && nwg % a.xcds == 0)
                          ? (int)(blockIdx.x % a.xcds) * (nwg / a.xcds) + (int)(blockIdx.x / a.xcds)
                          : (int)blockIdx.x;
-  const int head_base = blockIdx.y * (kHeadsPerWave * NW) + wave * kHeadsPerWave;
+  const bool s_owner = NHB == 4 || wave < NHB;  // runs S and the softmax of head block `wave`
+  const int head_base = blockIdx.y * (kHeadsPerWave * NHB) + wave * kHeadsPerWave;
   const int head = head_base + (lane & 31);
-  const bool head_ok = head < a.num_heads;
+  const bool head_ok = s_owner && head < a.num_heads;
   const int hi = lane >> 5;  // which half of the 32-token M block / k slots
 
   // ---- work range -------------------------------------------------------
@@ -524,15 +531,15 @@ void mla_partial_kernel(PartialArgs a) {
       seg.direct = g1 == g2;
     }
 
-    // O^T of this wave's dims: block j4 * NW + hb = dims 32 * j4 (of the
+    // O^T of this wave's dims: block j4 * NHB + hb = dims 32 * j4 (of the
     // wave's slice) x heads 32 * hb of the workgroup
-    f32x16 acc[NDB];
+    f32x16 acc[NACC];
 #pragma unroll
-    for (int d = 0; d < NDB; ++d) acc[d] = (f32x16)0.0f;
+    for (int d = 0; d < NACC; ++d) acc[d] = (f32x16)0.0f;
     float m_run = -INFINITY;  // base-2 reference max (per head)
     float l_run = 0.0f;       // sum of p over this lane's half of the tokens
     i16x8 qop[NKC];           // Q^T operands (B of S^T = K . Q^T), loaded below
-    i16x8 pop[2][NW];         // P^T operands of the sub-tile in PV: [c][hb]
+    i16x8 pop[2][NHB];        // P^T operands of the sub-tile in PV: [c][hb]
 
     // sub-tiles of 32 tokens; a trailing fully-invalid half tile is skipped
     const int st0 = 2 * seg.t0;
@@ -584,25 +591,29 @@ void mla_partial_kernel(PartialArgs a) {
     // PV steps [PV0, PV1) of O^T += V^T P^T for the sub-tile in vst, the
     // latter starting at step PVOFF, interleaved step by step so the MFMA
     // pipe alternates between the independent S chain and the PV
-    // accumulators. PV step g is MFMA (c, j4, hb) = (g / 16, (g % 16) / NW,
-    // g % NW); its V^T operand is read at the first hb of each j4 and its P^T
+    // accumulators. PV step g is MFMA (c, j4, hb) = (g / SPC, (g % SPC) / NHB,
+    // g % NHB), SPC = 4 * NHB steps per token half c; its V^T operand is
+    // read at the first hb of each j4 and its P^T
     // operand at the first j4 of each c. LDS operands run PD steps ahead;
     // each step waits with an lgkmcnt that counts exactly the reads issued
     // after its own. hook(step) runs after each step's MFMAs (copies of a
     // later sub-tile, the rescale check, softmax pieces), so its VALU and
     // memory work overlaps them.
     constexpr int PD = 2;
-    constexpr int PV_SPLIT = 16;  // PV steps beside S; the rest beside the softmax
-    constexpr int PV_START = 4;   // S-only steps first: the rescale factors arrive meanwhile
-    static_assert(PV_SPLIT % NW == 0 && PV_SPLIT >= 16, "a V^T operand never spans the two passes");
-    auto pass = [&](auto DOS, auto PVLO, auto PVHI, auto PVOFFC, const char LDS_AS* kst_v, const char LDS_AS* kst_r,
-                    const char LDS_AS* vst, const char LDS_AS* pst, f32x16& s, auto&& hook)
+    constexpr int SPC = NDBW * NHB;    // PV steps per token half
+    constexpr int PV_SPLIT = SPC;      // token half 0 beside S, half 1 beside the softmax
+    constexpr int PV_START = 4;        // S-only steps first: the rescale factors arrive meanwhile
+    constexpr int SM_STEPS = 11;       // steps the softmax pieces need in pass 2
+    static_assert(NDBW == 4, "four 32-dim blocks per wave");
+    auto pass = [&](auto DOS, auto PVLO, auto PVHI, auto PVOFFC, auto MINSTEPS, const char LDS_AS* kst_v,
+                    const char LDS_AS* kst_r, const char LDS_AS* vst, const char LDS_AS* pst, f32x16& s, auto&& hook)
                     __attribute__((always_inline)) {
       constexpr bool do_s = decltype(DOS)::value;
       constexpr int PV0 = decltype(PVLO)::value;
       constexpr int PVOFF = decltype(PVOFFC)::value;
       constexpr int NS = do_s ? NKC : 0, NV = decltype(PVHI)::value - PV0;
-      constexpr int NSTEPS = NS > NV + PVOFF ? NS : NV + PVOFF;
+      constexpr int NSTEPS0 = NS > NV + PVOFF ? NS : NV + PVOFF;
+      constexpr int NSTEPS = NSTEPS0 > decltype(MINSTEPS)::value ? NSTEPS0 : decltype(MINSTEPS)::value;
       const char LDS_AS* kvb[4] = {kst_v + k_off_v[0], kst_v + k_off_v[1], kst_v + k_off_v[2], kst_v + k_off_v[3]};
       const char LDS_AS* krb[4] = {kst_r + k_off_r[0], kst_r + k_off_r[1], kst_r + k_off_r[2], kst_r + k_off_r[3]};
       const char LDS_AS* vbase[2][2] = {{vst + v_off[0][0], vst + v_off[0][1]},
@@ -620,7 +631,7 @@ void mla_partial_kernel(PartialArgs a) {
             kb[t % (PD + 1)] = ds_read_b128<(cb - NVB) * 1024>(krb[t & 3]);
         }
         if constexpr (t >= PVOFF && t - PVOFF < NV) {
-          constexpr int g = PV0 + t - PVOFF, c = g / 16, j4 = (g % 16) / NW, hb = g % NW;
+          constexpr int g = PV0 + t - PVOFF, c = g / SPC, j4 = (g % SPC) / NHB, hb = g % NHB;
           if constexpr (hb == 0) {
             constexpr int off = c * 2 * NVB * 1024 + (j4 >> 1) * 1024;
             vl[c * NDBW + j4] = ds_read_tr<off>(vbase[j4 & 1][0]);
@@ -637,11 +648,11 @@ void mla_partial_kernel(PartialArgs a) {
         constexpr int last = (j + PD < NSTEPS - 1) ? j + PD : NSTEPS - 1;
         constexpr int after = [] {
           int n = 0;
-          for (int t = j + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NW, PVOFF>(t);
+          for (int t = j + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NHB, PVOFF>(t);
           return n;
         }();
         constexpr bool pv = j >= PVOFF && j - PVOFF < NV;
-        constexpr int g = PV0 + (pv ? j - PVOFF : 0), c = g / 16, j4 = (g % 16) / NW, hb = g % NW;
+        constexpr int g = PV0 + (pv ? j - PVOFF : 0), c = g / SPC, j4 = (g % SPC) / NHB, hb = g % NHB;
         constexpr bool has_k = j < NS;
         constexpr bool has_v = pv && hb == 0;
         constexpr bool has_p = pv && j4 == 0;
@@ -660,8 +671,8 @@ void mla_partial_kernel(PartialArgs a) {
         if constexpr (pv) {
           const i16x4 lo = vl[vi], hi4 = vh[vi];
           const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-          acc[j4 * NW + hb] = Elt<DT>::mfma(vop, pop[c][hb], acc[j4 * NW + hb]);
-          pin_agpr(acc[j4 * NW + hb]);
+          acc[j4 * NHB + hb] = Elt<DT>::mfma(vop, pop[c][hb], acc[j4 * NHB + hb]);
+          pin_agpr(acc[j4 * NHB + hb]);
         }
         hook(J);
       });
@@ -673,10 +684,10 @@ void mla_partial_kernel(PartialArgs a) {
     // in AGPRs.
     auto rescale = [&](const f32x4& alpha4) __attribute__((always_inline)) {
 #pragma unroll
-      for (int d = 0; d < NDB; ++d) {
+      for (int d = 0; d < NACC; ++d) {
         f32x16 t = acc[d];
         pin_vgpr(t);
-        t *= alpha4[d % NW];
+        t *= alpha4[d % NHB];
         acc[d] = t;
         pin_agpr(acc[d]);
       }
@@ -684,18 +695,21 @@ void mla_partial_kernel(PartialArgs a) {
 
     // P^T (and factor) buffers of the sub-tile before the first: P = 0 and
     // factor 1, so that iteration -1's PV half adds exactly nothing.
-    {
+    if (s_owner) {
       char LDS_AS* p1 = lds + OFF_P + PSLOT + wave * 2 * 1024 + lane * 16;
       ds_write_b128<0>(p1, (i16x8)0);
       ds_write_b128<1024>(p1, (i16x8)0);
       ds_write_b32(lds + OFF_A + ASLOT + ((lane & 31) * 4 + wave) * 4, 1.0f);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-    // Start-up, in the order the first iteration needs the data: page ids of
-    // the first kStages sub-tiles (scalar loads, issued before any vector
-    // traffic so they do not queue behind it; one wait), the copy of
-    // sub-tile 0, Q of this sequence, then the copies of sub-tiles 1 and 2.
+    // Start-up: page ids of the first kStages sub-tiles (scalar loads, issued
+    // before any vector traffic so they do not queue behind it; one wait),
+    // the copy of sub-tile 0 and Q, which iteration -1 needs, and once they
+    // have landed the copy of sub-tile 1; iteration -1 then copies sub-tile 2
+    // beside its MFMAs like every later iteration. At start-up every CU
+    // requests memory at once, so asking only for what is needed first lets
+    // the computation start sooner.
     static_assert(kStages == 4, "prologue page ids");
     int pro_page[kStages] = {0, 0, 0, 0};
     if (PAGED && PAGE_UNIFORM) {
@@ -705,7 +719,7 @@ void mla_partial_kernel(PartialArgs a) {
       for (int i = 0; i < kStages; ++i) pro_page[i] = page_ready(pro_page[i]);
     }
     issue(st0, pro_page[0]);  // nst >= 1
-    {
+    if (s_owner) {  // only the S waves use Q
       const short* qrow = reinterpret_cast<const short*>(a.q) + (int64_t)b * a.q_sb +
                           (int64_t)(head_ok ? head : 0) * a.q_sh + 8 * hi;
 #pragma unroll
@@ -714,20 +728,9 @@ void mla_partial_kernel(PartialArgs a) {
         qop[kc] = head_ok ? v : (i16x8)0;
       }
     }
-#pragma unroll
-    for (int i = 1; i < kStages - 1; ++i)
-      if (i < nst) issue(st0 + i, pro_page[i]);
-    // sub-tile 0 and Q have landed once at most the later copies are
-    // outstanding (vector loads complete in issue order); the loop then uses Q
-    // with no further wait
-    if (nst >= 3) {
-      wait_vmcnt<(2 * LOADS < 64 ? 2 * LOADS : 63)>();
-    } else if (nst == 2) {
-      wait_vmcnt<LOADS>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    int next_page = pro_page[kStages - 1];  // already waited for
+    wait_vmcnt<0>();  // sub-tile 0 and Q; the loop then uses Q with no further wait
+    if (nst > 1) issue(st0 + 1, pro_page[1]);
+    int next_page = pro_page[2];  // already waited for
 
     // Iteration i (-1 <= i < nst): PV(i) from ring entry i interleaved with
     // S(i+1) from entry i+1 (and the copies of sub-tile i+3), then the rest
@@ -737,8 +740,6 @@ void mla_partial_kernel(PartialArgs a) {
     // i = -1 the PV half multiplies sub-tile 0 by P = 0 and adds exactly
     // nothing; at i = nst-1 the S half reads a stale entry and its result is
     // discarded.
-    constexpr int COPY_STRIDE = NKC / LOADS;  // S steps per copy instruction
-    static_assert(NKC % LOADS == 0, "copies spread evenly over the S steps");
     for (int i = -1; i < nst; ++i) {
       // sub-tile i+1 must have landed; sub-tile i+2 may still be in flight
       if (i >= 0 && i + 1 < nst) {
@@ -748,7 +749,7 @@ void mla_partial_kernel(PartialArgs a) {
           wait_vmcnt<0>();
         }
       }
-      const bool do_copy = i >= 0 && i + kStages - 1 < nst;  // sub-tile i+3
+      const bool do_copy = i + kStages - 1 < nst;  // sub-tile i+3
       const int page = (PAGED && PAGE_UNIFORM && do_copy) ? page_ready(next_page) : 0;
       // every wave's P^T(i) and factors are written and every wave is done
       // with the ring entries refilled during this iteration
@@ -756,7 +757,8 @@ void mla_partial_kernel(PartialArgs a) {
       lds_barrier();
       // the page-id load goes out before every LDS read of the iteration, so
       // its out-of-order return can only make the counted waits wait longer
-      if (PAGED && PAGE_UNIFORM && i >= 0 && i + kStages < nst) next_page = page_fetch(st0 + i + kStages);
+      if (PAGED && PAGE_UNIFORM && i + kStages < nst)
+        next_page = i < 0 ? pro_page[kStages - 1] : page_fetch(st0 + i + kStages);
       const int pbuf = i & 1;
       f32x4 alpha4 = ds_read_f32x4(lds + OFF_A + pbuf * ASLOT + (lane & 31) * 16);
       const char LDS_AS* vst = lds + (i < 0 ? 0 : i % kStages) * VSLOT;
@@ -766,97 +768,126 @@ void mla_partial_kernel(PartialArgs a) {
       const int st_s = st0 + i + 1;  // sub-tile of this iteration's S
 
       // pass 1: S(i+1) and PV(i) steps [0, PV_SPLIT) from step PV_START on;
-      // the copies of sub-tile i+3 are spread over the S steps, and the
-      // factors published for PV(i) are applied before its first MFMA (the
-      // wait of step PV_START - 1 covers their read, which is older than
-      // every read of the pass)
+      // the copies of sub-tile i+3 are spread evenly over the pass's steps,
+      // and the factors published for PV(i) are applied before its first
+      // MFMA (the wait of step PV_START - 1 covers their read, which is older
+      // than every read of the pass)
       const char* csrc[RG_PER_WAVE];
-      auto pass1_hook = [&](auto J) __attribute__((always_inline)) {
-        constexpr int j = decltype(J)::value;
-        if constexpr (j == 0) {
-          if (do_copy) copy_src(st0 + i + kStages - 1, page, csrc);
-        }
-        if constexpr (j == PV_START - 1) {
-          pin_f4(alpha4);
-          bool any = false;
+      auto pass1_hook = [&](auto NSTEPSC) __attribute__((always_inline)) {
+        return [&](auto J) __attribute__((always_inline)) {
+          constexpr int j = decltype(J)::value;
+          constexpr int NST = decltype(NSTEPSC)::value;
+          if constexpr (j == 0) {
+            if (do_copy) copy_src(st0 + i + kStages - 1, page, csrc);
+          }
+          if constexpr (j == PV_START - 1) {
+            pin_f4(alpha4);
+            bool any = false;
 #pragma unroll
-          for (int hb = 0; hb < NW; ++hb) any |= alpha4[hb] != 1.0f;
-          if (__builtin_amdgcn_ballot_w64(any) != 0) rescale(alpha4);
-        }
-        if constexpr (j % COPY_STRIDE == COPY_STRIDE / 2 && j / COPY_STRIDE < LOADS) {
-          constexpr int idx = j / COPY_STRIDE;
-          if (do_copy) copy_one(st0 + i + kStages - 1, idx / NCB, std::integral_constant<int, idx % NCB>{}, csrc);
-        }
-      };
-      f32x16 s;
-      pass(std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
-           std::integral_constant<int, PV_START>{}, kst_v, kst_r, vst, pst, s, pass1_hook);
+            for (int hb = 0; hb < NHB; ++hb) any |= alpha4[hb] != 1.0f;
+            if (__builtin_amdgcn_ballot_w64(any) != 0) rescale(alpha4);
+          }
+          static_for<LOADS>([&](auto K) __attribute__((always_inline)) {
+            constexpr int k = decltype(K)::value;
+            if constexpr (k * NST / LOADS == j) {
+              if (do_copy) copy_one(st0 + i + kStages - 1, k / NCB, std::integral_constant<int, k % NCB>{}, csrc);
+            }
+          });
 
-      // pass 2: PV(i) steps [PV_SPLIT, 2 * NDB) beside the softmax of
-      // sub-tile i+1 (heads of this wave), base-2 with the lazy rescale: the
-      // reference max only moves, for the whole wave, when a score exceeds
-      // it by 2^kRescaleLog2 (then both token halves of every head agree on
-      // the new max through one lane exchange). Scores stay unscaled: the
-      // max is taken on s (scale > 0) or -s (scale < 0) and the scale is
-      // folded into p = 2^(s * c - m).
-      const bool full = (st_s + 1) * kSubTokens <= n_b;  // no token past the sequence
-      const float c = a.qk_scale_log2;
-      float m_use = m_run, lsum = 0.0f, alpha = 1.0f;
-      i16x8 pnext[2];
-      auto softmax_hook = [&](auto J) __attribute__((always_inline)) {
-        constexpr int j = decltype(J)::value;
-        if constexpr (j == 0) {  // mask tokens past the sequence (last sub-tile only)
-          if (!full) {
-            const int tok0 = st_s * kSubTokens + 4 * hi;
-            const float off = c >= 0.0f ? -INFINITY : INFINITY;
+        };
+      };
+
+      // S-owner waves: pass 1 with S(i+1); pass 2 = PV(i) steps
+      // [PV_SPLIT, 2 * SPC) beside the softmax of sub-tile i+1 (heads of this
+      // wave), base-2 with the lazy rescale: the reference max only moves,
+      // for the whole wave, when a score exceeds it by 2^kRescaleLog2 (then
+      // both token halves of every head agree on the new max through one lane
+      // exchange). Scores stay unscaled: the max is taken on s (scale > 0) or
+      // -s (scale < 0) and the scale is folded into p = 2^(s * c - m).
+      auto owner_iteration = [&]() __attribute__((always_inline)) {
+        f32x16 s;
+        pass(std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
+             std::integral_constant<int, PV_START>{}, std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s,
+             pass1_hook(std::integral_constant<int, NKC>{}));
+        const bool full = (st_s + 1) * kSubTokens <= n_b;  // no token past the sequence
+        const float c = a.qk_scale_log2;
+        float m_use = m_run, lsum = 0.0f, alpha = 1.0f;
+        i16x8 pnext[2];
+        auto softmax_hook = [&](auto J) __attribute__((always_inline)) {
+          constexpr int j = decltype(J)::value;
+          if constexpr (j == 0) {  // mask tokens past the sequence (last sub-tile only)
+            if (!full) {
+              const int tok0 = st_s * kSubTokens + 4 * hi;
+              const float off = c >= 0.0f ? -INFINITY : INFINITY;
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-              if (tok0 + 8 * (r >> 2) + (r & 3) >= n_b) s[r] = off;
+              for (int r = 0; r < 16; ++r)
+                if (tok0 + 8 * (r >> 2) + (r & 3) >= n_b) s[r] = off;
+            }
+            pin_f16(s);
+          } else if constexpr (j == 1) {  // reference max
+            float mx = c >= 0.0f ? s[0] : -s[0];
+            if (c >= 0.0f) {
+#pragma unroll
+              for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+            } else {
+#pragma unroll
+              for (int r = 1; r < 16; ++r) mx = fmaxf(mx, -s[r]);
+            }
+            mx *= fabsf(c);
+            if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleLog2) != 0) {
+              // the exchange is an LDS operation outside the pass's
+              // counting: let every counted read finish first
+              asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+              m_use = fmaxf(m_run, fmaxf(mx, __shfl_xor(mx, 32)));
+              if (m_run != -INFINITY) alpha = fast_exp2(m_run - m_use);
+            }
+            pin_f2(m_use, alpha);
+          } else if constexpr (j >= 2 && j < 10) {  // two probabilities
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const int r = 2 * (j - 2) + e;
+              s[r] = fast_exp2(fmaf(s[r], c, -m_use));  // masked: +-inf * c = -inf -> 0
+              lsum += s[r];
+            }
+            pin_f16(s);
+            pin_f1(lsum);
+          } else if constexpr (j == 10) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pnext[r >> 3][r & 7] = Elt<DT>::from_float(s[r]);
           }
-          pin_f16(s);
-        } else if constexpr (j == 1) {  // reference max
-          float mx = c >= 0.0f ? s[0] : -s[0];
-          if (c >= 0.0f) {
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-          } else {
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, -s[r]);
-          }
-          mx *= fabsf(c);
-          if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleLog2) != 0) {
-            // the exchange is an LDS operation outside the pass's
-            // counting: let every counted read finish first
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            m_use = fmaxf(m_run, fmaxf(mx, __shfl_xor(mx, 32)));
-            if (m_run != -INFINITY) alpha = fast_exp2(m_run - m_use);
-          }
-          pin_f2(m_use, alpha);
-        } else if constexpr (j >= 2 && j < 10) {  // two probabilities
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int r = 2 * (j - 2) + e;
-            s[r] = fast_exp2(fmaf(s[r], c, -m_use));  // masked: +-inf * c = -inf -> 0
-            lsum += s[r];
-          }
-          pin_f16(s);
-          pin_f1(lsum);
-        } else if constexpr (j == 10) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) pnext[r >> 3][r & 7] = Elt<DT>::from_float(s[r]);
+        };
+        static_assert(SM_STEPS == 11, "softmax pieces 0..10");
+        pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * SPC>{},
+             std::integral_constant<int, 0>{}, std::integral_constant<int, SM_STEPS>{}, kst_v, kst_r, vst, pst, s,
+             softmax_hook);
+        {
+          char LDS_AS* pw = lds + OFF_P + (pbuf ^ 1) * PSLOT + wave * 2 * 1024 + lane * 16;
+          ds_write_b128<0>(pw, pnext[0]);
+          ds_write_b128<1024>(pw, pnext[1]);
+          ds_write_b32(lds + OFF_A + (pbuf ^ 1) * ASLOT + ((lane & 31) * 4 + wave) * 4, alpha);
+        }
+        if (i + 1 < nst) {
+          l_run = l_run * alpha + lsum;
+          m_run = m_use;
         }
       };
-      pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * NDB>{},
-           std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s, softmax_hook);
-      {
-        char LDS_AS* pw = lds + OFF_P + (pbuf ^ 1) * PSLOT + wave * 2 * 1024 + lane * 16;
-        ds_write_b128<0>(pw, pnext[0]);
-        ds_write_b128<1024>(pw, pnext[1]);
-        ds_write_b32(lds + OFF_A + (pbuf ^ 1) * ASLOT + ((lane & 31) * 4 + wave) * 4, alpha);
-      }
-      if (i + 1 < nst) {
-        l_run = l_run * alpha + lsum;
-        m_run = m_use;
+      // the other waves: their share of PV(i) and of the copies
+      auto pv_iteration = [&]() __attribute__((always_inline)) {
+        f32x16 s;
+        pass(std::false_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
+             std::integral_constant<int, PV_START>{}, std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s,
+             pass1_hook(std::integral_constant<int, PV_SPLIT + PV_START>{}));
+        pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * SPC>{},
+             std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s,
+             [](auto) {});
+      };
+      if constexpr (NHB == NW) {
+        owner_iteration();
+      } else {
+        if (s_owner)
+          owner_iteration();
+        else
+          pv_iteration();
       }
     }
     // all waves must be done with the rings before they are reused below
@@ -874,18 +905,18 @@ void mla_partial_kernel(PartialArgs a) {
       lds_barrier();
       f32x4 inv4 = ds_read_f32x4(lds + OFF_A + (lane & 31) * 16);
       lgkm_tie_f4<0>(inv4);
-      // The normalised rows go through the idle rings (32*NW padded rows;
+      // The normalised rows go through the idle rings (32*NHB padded rows;
       // the 16-byte pad spreads the lanes' 8-byte writes over all banks),
       // so that every global store then writes one whole row of DV elements.
 #pragma unroll
       for (int j4 = 0; j4 < NDBW; ++j4)
 #pragma unroll
-        for (int hb = 0; hb < NW; ++hb)
+        for (int hb = 0; hb < NHB; ++hb)
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
             i16x4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = Elt<DT>::from_float(acc[j4 * NW + hb][4 * q4 + e] * inv4[hb]);
+            for (int e = 0; e < 4; ++e) v[e] = Elt<DT>::from_float(acc[j4 * NHB + hb][4 * q4 + e] * inv4[hb]);
             const int dim = wave * (DV / NW) + 32 * j4 + 8 * q4 + 4 * hi;
             *reinterpret_cast<i16x4 LDS_AS*>(lds + (hb * 32 + (lane & 31)) * OPITCH + dim * 2) = v;
           }
@@ -1082,23 +1113,23 @@ int check_common(const Common& c, const void* workspace, size_t ws_bytes) {
   return TMLA_OK;
 }
 
-template <int DT, int NW, bool PAGED, bool UNI>
+template <int DT, int NHB, bool PAGED, bool UNI>
 hipError_t launch_partial_t(const PartialArgs& a, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((mla_partial_kernel<DT, 512, 64, NW, PAGED, UNI>), grid, dim3(64 * NW), 0, stream, a);
+  hipLaunchKernelGGL((mla_partial_kernel<DT, 512, 64, NHB, PAGED, UNI>), grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
-template <int DT, int NW>
+template <int DT, int NHB>
 hipError_t launch_partial_nw(const PartialArgs& a, dim3 grid, hipStream_t stream, bool paged, bool uni) {
-  if (!paged) return launch_partial_t<DT, NW, false, false>(a, grid, stream);
-  if (uni) return launch_partial_t<DT, NW, true, true>(a, grid, stream);
-  return launch_partial_t<DT, NW, true, false>(a, grid, stream);
+  if (!paged) return launch_partial_t<DT, NHB, false, false>(a, grid, stream);
+  if (uni) return launch_partial_t<DT, NHB, true, true>(a, grid, stream);
+  return launch_partial_t<DT, NHB, true, false>(a, grid, stream);
 }
 
 template <int DT>
-hipError_t launch_partial_dt(const PartialArgs& a, dim3 grid, int nw, hipStream_t stream, bool paged, bool uni) {
-  if (nw == 1) return launch_partial_nw<DT, 1>(a, grid, stream, paged, uni);
-  if (nw == 2) return launch_partial_nw<DT, 2>(a, grid, stream, paged, uni);
+hipError_t launch_partial_dt(const PartialArgs& a, dim3 grid, int nhb, hipStream_t stream, bool paged, bool uni) {
+  if (nhb == 1) return launch_partial_nw<DT, 1>(a, grid, stream, paged, uni);
+  if (nhb == 2) return launch_partial_nw<DT, 2>(a, grid, stream, paged, uni);
   return launch_partial_nw<DT, 4>(a, grid, stream, paged, uni);
 }
 
@@ -1178,15 +1209,16 @@ int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_
   a.mid_o = reinterpret_cast<short*>(ws);
   a.mid_lse = reinterpret_cast<float*>(ws + (((size_t)slots * num_heads * 512 * 2 + 255) & ~(size_t)255));
 
-  const int nw = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
-  const int heads_per_wg = 32 * nw;
+  // blocks of 32 heads per workgroup (4 waves in every case)
+  const int nhb = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
+  const int heads_per_wg = 32 * nhb;
   const int workers = num_splits > 0 ? batch * num_splits : num_workers;
   dim3 grid(workers, (num_heads + heads_per_wg - 1) / heads_per_wg);
   // one page per 32-token sub-tile: sub-tiles never straddle a page
   const bool uni = paged && (page_size % kSubTokens == 0);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = dtype == TMLA_BF16 ? launch_partial_dt<TMLA_BF16>(a, grid, nw, s, paged, uni)
-                                    : launch_partial_dt<TMLA_FP16>(a, grid, nw, s, paged, uni);
+  hipError_t e = dtype == TMLA_BF16 ? launch_partial_dt<TMLA_BF16>(a, grid, nhb, s, paged, uni)
+                                    : launch_partial_dt<TMLA_FP16>(a, grid, nhb, s, paged, uni);
   if (e != hipSuccess) return hip_fail(e, "mla_partial_kernel launch");
   return TMLA_OK;
 }
