@@ -105,6 +105,17 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
+// The lane id through an instruction the compiler cannot look through:
+// offsets derived from it are recomputed where they are needed instead of
+// being kept live across the whole kernel (where they would be spilled to
+// scratch and reloaded, one memory round trip each, at start-up and in the
+// finalize).
+__device__ __forceinline__ int lane_id_fresh() {
+  int v;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(v));
+  return v;
+}
+
 // Register-class pins: an empty asm that requires its operand in VGPRs /
 // AGPRs at that point. They keep the PV accumulators in AGPRs and the S tile
 // in VGPRs instead of letting the allocator shuttle blocks between files.
@@ -244,9 +255,12 @@ __device__ __forceinline__ void mfma_vgpr_fence(f32x16& d) {
 
 // 16-byte store written through to memory (sc0 sc1: system-scope write-
 // through), so a kernel that ends with many such stores leaves no dirty L2
-// lines for the end-of-kernel write-back.
+// lines for the end-of-kernel write-back. The s_nop supplies the wait state
+// the hardware needs before a VALU instruction may overwrite the data VGPRs
+// of a store wider than 64 bits: the compiler inserts it for the stores it
+// generates, but cannot see into this asm.
 __device__ __forceinline__ void store_through(i16x8* p, i16x8 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" : : "v"(p), "v"(v) : "memory");
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
 }
 
 // One LDS-DMA copy: 16 bytes per lane from src + OFF into LDS at
@@ -383,12 +397,9 @@ void mla_partial_kernel(PartialArgs a) {
   static_assert(DV == 512, "one output row = 64 lanes x 8 elements");
 
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
-  __shared__ int s_info[4];
-  int* const s_scan = reinterpret_cast<int*>(smem);  // start-up only, before any copy
   char LDS_AS* const lds = (char LDS_AS*)(void LDS_AS*)smem;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar LDS bases
   // Logical worker index: consecutive workers (the pieces of one sequence,
   // which share its Q rows and write neighbouring partial slots) are placed
@@ -400,9 +411,6 @@ void mla_partial_kernel(PartialArgs a) {
                          : (int)blockIdx.x;
   const bool s_owner = NHB == 4 || wave < NHB;  // runs S and the softmax of head block `wave`
   const int head_base = blockIdx.y * (kHeadsPerWave * NHB) + wave * kHeadsPerWave;
-  const int head = head_base + (lane & 31);
-  const bool head_ok = s_owner && head < a.num_heads;
-  const int hi = lane >> 5;  // which half of the 32-token M block / k slots
 
   // ---- work range -------------------------------------------------------
   int b_first, tile_lo, tile_hi, off_first, n_first, chunk = 0;
@@ -418,88 +426,45 @@ void mla_partial_kernel(PartialArgs a) {
     off_first = 0;
   } else {
     // Balanced: the T tiles of all sequences (in order) are cut into
-    // num_workers ranges of c = cdiv(T, num_workers) tiles.
-    const int nthreads = 64 * NW;
-    const int per = (a.batch + nthreads - 1) / nthreads;
-    const int lo_b = min(tid * per, a.batch), hi_b = min(lo_b + per, a.batch);
-    // the first length of this thread's chunk stays in a register for the
-    // search below (with batch <= 64 * NW that is the whole chunk)
+    // num_workers ranges of c = cdiv(T, num_workers) tiles. Every wave
+    // computes the partition on its own (registers and cross-lane moves
+    // only, no LDS or barrier): lane l sums the tile counts of sequences
+    // [l * per, (l + 1) * per), a wave-wide inclusive scan gives each lane
+    // the tile offset where its sequences end.
+    const int lane0 = lane_id_fresh();
+    const int per = (a.batch + 63) >> 6;
+    const int lo_b = min(lane0 * per, a.batch), hi_b = min(lo_b + per, a.batch);
     const int len0 = lo_b < hi_b ? a.seqlens[lo_b] : 0;
     int sum = tiles_of(len0);
     for (int b = lo_b + 1; b < hi_b; ++b) sum += tiles_of(a.seqlens[b]);
-    s_scan[tid] = sum;
-    __syncthreads();
-    // inclusive scan over the per-thread chunk sums (Hillis-Steele in LDS)
-    for (int d = 1; d < nthreads; d <<= 1) {
-      const int v = tid >= d ? s_scan[tid - d] : 0;
-      __syncthreads();
-      s_scan[tid] += v;
-      __syncthreads();
+    int incl = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d);
+      if (lane0 >= d) incl += v;
     }
-    const int total = __builtin_amdgcn_readfirstlane(s_scan[nthreads - 1]);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
     chunk = (total + a.num_workers - 1) / a.num_workers;
     const int lo = worker * chunk;
-    if (tid == 0) s_info[0] = -1;
-    __syncthreads();
-    if (lo < total) {
-      int off = s_scan[tid] - sum;  // exclusive prefix of this thread's chunk
-      if (off <= lo && lo < off + sum) {
-        for (int b = lo_b; b < hi_b; ++b) {
-          const int len = b == lo_b ? len0 : a.seqlens[b];
-          const int nt = tiles_of(len);
-          if (lo < off + nt) {
-            s_info[0] = b;
-            s_info[1] = off;
-            s_info[2] = len;
-            break;
-          }
-          off += nt;
-        }
-      }
+    if (lo >= total) return;  // wave-uniform, and the same in every wave
+    // the one lane whose sequences hold tile lo finds which of them it is
+    int off = incl - sum, fb = lo_b, flen = len0;
+    for (int b = lo_b; b < hi_b; ++b) {
+      const int len = b == lo_b ? len0 : a.seqlens[b];
+      const int nt = tiles_of(len);
+      fb = b;
+      flen = len;
+      if (lo < off + nt) break;
+      off += nt;
     }
-    __syncthreads();
-    if (s_info[0] < 0) return;
-    b_first = __builtin_amdgcn_readfirstlane(s_info[0]);
-    off_first = __builtin_amdgcn_readfirstlane(s_info[1]);
-    n_first = __builtin_amdgcn_readfirstlane(s_info[2]);
-    tile_lo = lo - off_first;  // local to b_first
+    const int src = __builtin_ctzll(__ballot(sum > 0 && incl - sum <= lo && lo < incl));
+    b_first = __builtin_amdgcn_readlane(fb, src);
+    off_first = __builtin_amdgcn_readlane(off, src);
+    n_first = __builtin_amdgcn_readlane(flen, src);
+    tile_lo = lo - off_first;                      // local to b_first
     tile_hi = min(lo + chunk, total) - off_first;  // may run past b_first
-    __syncthreads();  // the scan lives where the first copies land
   }
   if (tile_lo >= tile_hi) return;
-
-  // per-lane LDS read offsets inside a ring entry
-  // S^T A operand: token = lane%32 (rg = (lane%32)/8, r = lane%8), piece = 2*(kc%4) + hi
-  int k_off_v[4], k_off_r[4];
-  {
-    const int rg = (lane & 31) >> 3, r = lane & 7;
-    const int sw = piece_swizzle(r, rg);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int in_block = (r * 8 + ((2 * j + hi) ^ sw)) * 16;
-      k_off_v[j] = rg * NVB * 1024 + in_block;
-      k_off_r[j] = OFF_R + rg * NRB * 1024 + in_block;
-    }
-  }
-  // V^T operand via ds_read_b64_tr_b16: group g = lane/16, L = lane%16;
-  // read e2 covers tokens 16c + 8e2 + 4(g/2) + L/4, dims 32db + 16(g%2) + 4(L%4).
-  // This wave's dims start at block column (wave * NDBW / 2).
-  int v_off[2][2];  // [db&1][e2]
-  {
-    const int g = lane >> 4, L = lane & 15;
-    const int r = 4 * (g >> 1) + (L >> 2);
-#pragma unroll
-    for (int dbp = 0; dbp < 2; ++dbp)
-#pragma unroll
-      for (int e2 = 0; e2 < 2; ++e2) {
-        const int piece = 4 * dbp + 2 * (g & 1) + ((L & 3) >> 1);
-        v_off[dbp][e2] = e2 * NVB * 1024 + wave * (NDBW / 2) * 1024 +
-                         (r * 8 + (piece ^ piece_swizzle(r, e2))) * 16 + 8 * (L & 1);
-      }
-  }
-  // DMA: this lane copies, for each of its wave's row-groups, the piece
-  // (lane%8) ^ swizzle of token row 8rg + lane/8.
-  const int dma_r = lane >> 3;
 
   // ---- segments -----------------------------------------------------------
   int b = b_first;
@@ -515,6 +480,45 @@ void mla_partial_kernel(PartialArgs a) {
       continue;
     }
     const int t_end = min(nt_b, t_start + remaining);
+    // this segment's lane-derived values (recomputed per segment, see
+    // lane_id_fresh)
+    const int lane = lane_id_fresh();
+    const int head = head_base + (lane & 31);
+    const bool head_ok = s_owner && head < a.num_heads;
+    const int hi = lane >> 5;  // which half of the 32-token M block / k slots
+    // per-lane LDS read offsets inside a ring entry
+    // S^T A operand: token = lane%32 (rg = (lane%32)/8, r = lane%8), piece = 2*(kc%4) + hi
+    int k_off_v[4], k_off_r[4];
+    {
+      const int rg = (lane & 31) >> 3, r = lane & 7;
+      const int sw = piece_swizzle(r, rg);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int in_block = (r * 8 + ((2 * j + hi) ^ sw)) * 16;
+        k_off_v[j] = rg * NVB * 1024 + in_block;
+        k_off_r[j] = OFF_R + rg * NRB * 1024 + in_block;
+      }
+    }
+    // V^T operand via ds_read_b64_tr_b16: group g = lane/16, L = lane%16;
+    // read e2 covers tokens 16c + 8e2 + 4(g/2) + L/4, dims 32db + 16(g%2) + 4(L%4).
+    // This wave's dims start at block column (wave * NDBW / 2).
+    int v_off[2][2];  // [db&1][e2]
+    {
+      const int g = lane >> 4, L = lane & 15;
+      const int r = 4 * (g >> 1) + (L >> 2);
+#pragma unroll
+      for (int dbp = 0; dbp < 2; ++dbp)
+#pragma unroll
+        for (int e2 = 0; e2 < 2; ++e2) {
+          const int piece = 4 * dbp + 2 * (g & 1) + ((L & 3) >> 1);
+          v_off[dbp][e2] = e2 * NVB * 1024 + wave * (NDBW / 2) * 1024 +
+                           (r * 8 + (piece ^ piece_swizzle(r, e2))) * 16 + 8 * (L & 1);
+        }
+    }
+    // DMA: this lane copies, for each of its wave's row-groups, the piece
+    // (lane%8) ^ swizzle of token row 8rg + lane/8.
+    const int dma_r = lane >> 3;
+
     Segment seg;
     seg.b = b;
     seg.t0 = t_start;
@@ -704,31 +708,33 @@ void mla_partial_kernel(PartialArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
     // Start-up: page ids of the first kStages sub-tiles (scalar loads, issued
-    // before any vector traffic so they do not queue behind it; one wait),
-    // the copy of sub-tile 0 and Q, which iteration -1 needs, and once they
-    // have landed the copy of sub-tile 1; iteration -1 then copies sub-tile 2
-    // beside its MFMAs like every later iteration. At start-up every CU
-    // requests memory at once, so asking only for what is needed first lets
-    // the computation start sooner.
+    // before any vector traffic so they do not queue behind it), Q (needs
+    // no page id, so it is in flight while the page ids come back), the copy
+    // of sub-tile 0, and once Q and sub-tile 0 have landed the copy of
+    // sub-tile 1; iteration -1 then copies sub-tile 2 beside its MFMAs like
+    // every later iteration. At start-up every CU requests memory at once,
+    // so asking only for what is needed first lets the computation start
+    // sooner.
     static_assert(kStages == 4, "prologue page ids");
     int pro_page[kStages] = {0, 0, 0, 0};
     if (PAGED && PAGE_UNIFORM) {
 #pragma unroll
       for (int i = 0; i < kStages; ++i) pro_page[i] = page_fetch(st0 + min(i, nst - 1));
+    }
+    if (s_owner) {  // only the S waves use Q
+      // heads past num_heads (a partial last block) run on head 0's row:
+      // their scores stay finite and their output rows are never stored
+      const short* qrow = reinterpret_cast<const short*>(a.q) + (int64_t)b * a.q_sb +
+                          (int64_t)(head_ok ? head : 0) * a.q_sh + 8 * hi;
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) qop[kc] = *reinterpret_cast<const i16x8*>(qrow + 16 * kc);
+    }
+    if (PAGED && PAGE_UNIFORM) {
 #pragma unroll
       for (int i = 0; i < kStages; ++i) pro_page[i] = page_ready(pro_page[i]);
     }
     issue(st0, pro_page[0]);  // nst >= 1
-    if (s_owner) {  // only the S waves use Q
-      const short* qrow = reinterpret_cast<const short*>(a.q) + (int64_t)b * a.q_sb +
-                          (int64_t)(head_ok ? head : 0) * a.q_sh + 8 * hi;
-#pragma unroll
-      for (int kc = 0; kc < NKC; ++kc) {
-        i16x8 v = *reinterpret_cast<const i16x8*>(qrow + 16 * kc);
-        qop[kc] = head_ok ? v : (i16x8)0;
-      }
-    }
-    wait_vmcnt<0>();  // sub-tile 0 and Q; the loop then uses Q with no further wait
+    wait_vmcnt<0>();  // Q and sub-tile 0; the loop then uses Q with no further wait
     if (nst > 1) issue(st0 + 1, pro_page[1]);
     int next_page = pro_page[2];  // already waited for
 
@@ -894,61 +900,73 @@ void mla_partial_kernel(PartialArgs a) {
     lds_barrier();
 
     // ---- finalize: out = acc / l, lse2 = m + log2(l) -------------------------
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
-    const bool has = l_tot > 0.0f;
-    const float inv = has ? 1.0f / l_tot : 0.0f;
-    const float lse2 = has ? m_run + fast_log2(l_tot) : -INFINITY;
     {
-      // 1/l of every head of the workgroup, for the waves' column slices
-      ds_write_b32(lds + OFF_A + ((lane & 31) * 4 + wave) * 4, inv);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      lds_barrier();
-      f32x4 inv4 = ds_read_f32x4(lds + OFF_A + (lane & 31) * 16);
-      lgkm_tie_f4<0>(inv4);
-      // The normalised rows go through the idle rings (32*NHB padded rows;
-      // the 16-byte pad spreads the lanes' 8-byte writes over all banks),
-      // so that every global store then writes one whole row of DV elements.
+      const int lane = lane_id_fresh();  // (see lane_id_fresh)
+      const int head = head_base + (lane & 31);
+      const bool head_ok = s_owner && head < a.num_heads;
+      const int hi = lane >> 5;
+      const float l_tot = l_run + __shfl_xor(l_run, 32);
+      const bool has = l_tot > 0.0f;
+      const float inv = has ? 1.0f / l_tot : 0.0f;
+      const float lse2 = has ? m_run + fast_log2(l_tot) : -INFINITY;
+      {
+        // 1/l of every head of the workgroup, for the waves' column slices
+        ds_write_b32(lds + OFF_A + ((lane & 31) * 4 + wave) * 4, inv);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_barrier();
+        f32x4 inv4 = ds_read_f32x4(lds + OFF_A + (lane & 31) * 16);
+        lgkm_tie_f4<0>(inv4);
+        // The normalised rows go through the idle rings (32*NHB padded rows;
+        // the 16-byte pad spreads the lanes' 8-byte writes over all banks),
+        // so that every global store then writes one whole row of DV elements.
 #pragma unroll
-      for (int j4 = 0; j4 < NDBW; ++j4)
+        for (int j4 = 0; j4 < NDBW; ++j4)
 #pragma unroll
-        for (int hb = 0; hb < NHB; ++hb)
+          for (int hb = 0; hb < NHB; ++hb)
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            i16x4 v;
+            for (int q4 = 0; q4 < 4; ++q4) {
+              i16x4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = Elt<DT>::from_float(acc[j4 * NHB + hb][4 * q4 + e] * inv4[hb]);
-            const int dim = wave * (DV / NW) + 32 * j4 + 8 * q4 + 4 * hi;
-            *reinterpret_cast<i16x4 LDS_AS*>(lds + (hb * 32 + (lane & 31)) * OPITCH + dim * 2) = v;
-          }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      lds_barrier();
-      short* dst;
-      int64_t row_stride;
-      if (seg.direct) {
-        dst = reinterpret_cast<short*>(a.out) + (int64_t)b * a.out_sb + (int64_t)head_base * a.out_sh;
-        row_stride = a.out_sh;
-      } else {
-        // the partial is a convex combination of cache rows, so it fits the
-        // input dtype; it is stored there (half the bytes of float32)
-        dst = a.mid_o + ((int64_t)seg.slot * a.num_heads + head_base) * DV;
-        row_stride = DV;
+              for (int e = 0; e < 4; ++e) v[e] = Elt<DT>::from_float(acc[j4 * NHB + hb][4 * q4 + e] * inv4[hb]);
+              const int dim = wave * (DV / NW) + 32 * j4 + 8 * q4 + 4 * hi;
+              *reinterpret_cast<i16x4 LDS_AS*>(lds + (hb * 32 + (lane & 31)) * OPITCH + dim * 2) = v;
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_barrier();
+        short* dst;
+        int64_t row_stride;
+        if (seg.direct) {
+          dst = reinterpret_cast<short*>(a.out) + (int64_t)b * a.out_sb + (int64_t)head_base * a.out_sh;
+          row_stride = a.out_sh;
+        } else {
+          // the partial is a convex combination of cache rows, so it fits the
+          // input dtype; it is stored there (half the bytes of float32)
+          dst = a.mid_o + ((int64_t)seg.slot * a.num_heads + head_base) * DV;
+          row_stride = DV;
+        }
+        const int rows = min(32, a.num_heads - head_base);  // wave-uniform
+        const char LDS_AS* obuf = lds + wave * 32 * OPITCH;
+        // eight rows per batch: their reads are all issued before the first
+        // store waits for its data
+#pragma unroll
+        for (int r0 = 0; r0 < 32; r0 += 8) {
+          i16x8 row[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) row[k] = *reinterpret_cast<const i16x8 LDS_AS*>(obuf + (r0 + k) * OPITCH + lane * 16);
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            if (r0 + k < rows) store_through(reinterpret_cast<i16x8*>(dst + (r0 + k) * row_stride + lane * 8), row[k]);
+        }
+        if (head_ok && hi == 0) {
+          if (seg.direct)
+            a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
+          else
+            a.mid_lse[(int64_t)seg.slot * a.num_heads + head] = lse2;
+        }
+        // the next segment refills the rings
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_barrier();
       }
-      const int rows = min(32, a.num_heads - head_base);  // wave-uniform
-      const char LDS_AS* obuf = lds + wave * 32 * OPITCH;
-#pragma unroll
-      for (int r = 0; r < 32; ++r)
-        if (r < rows)
-          store_through(reinterpret_cast<i16x8*>(dst + r * row_stride + lane * 8),
-                        *reinterpret_cast<const i16x8 LDS_AS*>(obuf + r * OPITCH + lane * 16));
-      if (head_ok && hi == 0) {
-        if (seg.direct)
-          a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
-        else
-          a.mid_lse[(int64_t)seg.slot * a.num_heads + head] = lse2;
-      }
-      // the next segment refills the rings
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      lds_barrier();
     }
 
     remaining -= (t_end - t_start);
