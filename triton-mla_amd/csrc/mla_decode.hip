@@ -62,6 +62,7 @@ struct PartialArgs {
   const char* kv;
   int64_t kv_s0, kv_s1;    // byte strides: block (dense: batch), token
   int64_t num_blocks;
+  int32_t max_page;               // min(num_blocks - 1, INT32_MAX): page ids are clamped to it
   int32_t page_size, page_shift;  // page_shift = log2(page_size) or -1
   const int32_t* bt;
   int64_t bt_sb;
@@ -326,15 +327,17 @@ __device__ __forceinline__ int64_t row_offset(const PartialArgs& a, int b, int t
   return (int64_t)page_id * a.kv_s0 + (int64_t)in_page * a.kv_s1;
 }
 
+// POW2: the page size is known to be a power of two (page_shift >= 0)
+template <bool POW2 = false>
 __device__ __forceinline__ int page_slot_of(const PartialArgs& a, int t) {
-  const int s = a.page_shift >= 0 ? (t >> a.page_shift) : (t / a.page_size);
+  const int s = (POW2 || a.page_shift >= 0) ? (t >> a.page_shift) : (t / a.page_size);
   return min(s, a.bt_cols - 1);
 }
 
 __device__ __forceinline__ int load_page(const PartialArgs& a, int b, int slot) {
   int p = a.bt[(int64_t)b * a.bt_sb + slot];
   p = p < 0 ? 0 : p;
-  return (int64_t)p >= a.num_blocks ? (int)(a.num_blocks - 1) : p;
+  return min(p, a.max_page);
 }
 
 // Segment of a worker: tiles [t0, t1) of sequence b, result goes to `slot`
@@ -365,6 +368,7 @@ struct Segment {
 //    of all 32*NHB heads, so each V^T operand read from LDS feeds NHB MFMAs.
 // With fewer than 4 head blocks the waves past NHB only copy and run PV, so
 // small head counts still use every SIMD of the CU.
+// PAGE_UNIFORM: paged, page size a power of two and a multiple of 32
 template <int DT, int DV, int DR, int NHB, bool PAGED, bool PAGE_UNIFORM>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void mla_partial_kernel(PartialArgs a) {
@@ -555,18 +559,35 @@ void mla_partial_kernel(PartialArgs a) {
     // needs it, so its wait is free when it comes.
     const int32_t* bt_row = PAGED ? a.bt + (int64_t)b * a.bt_sb : a.bt;
     auto page_fetch = [&](int st) __attribute__((always_inline)) -> int {
-      return s_load_i32(bt_row + page_slot_of(a, st * kSubTokens));
+      return s_load_i32(bt_row + page_slot_of<PAGE_UNIFORM>(a, st * kSubTokens));
     };
     auto page_ready = [&](int v) __attribute__((always_inline)) -> int {
       v = s_wait_i32(v);
-      return v < 0 ? 0 : ((int64_t)v >= a.num_blocks ? (int)(a.num_blocks - 1) : v);
+      return v < 0 ? 0 : min(v, a.max_page);
     };
 
     // Copies of one sub-tile: per-lane source rows (one per row-group of this
     // wave, already offset to this lane's 16-byte piece), then one
     // global_load_lds per (row-group, column block).
+    // A whole sub-tile inside one page (every sub-tile but a sequence's last,
+    // partial one) needs no clamping: its rows start at a uniform offset
+    // (page, first row in the page) plus a per-lane offset that is the same
+    // for every sub-tile of the segment.
+    int64_t lane_row_off[RG_PER_WAVE];
+#pragma unroll
+    for (int ri = 0; ri < RG_PER_WAVE; ++ri) {
+      const int rg = wave * RG_PER_WAVE + ri;
+      lane_row_off[ri] = (int64_t)(rg * 8 + dma_r) * a.kv_s1 + ((lane & 7) ^ piece_swizzle(dma_r, rg)) * 16;
+    }
     auto copy_src = [&](int st, int page, const char* (&src)[RG_PER_WAVE]) __attribute__((always_inline)) {
       const int tok_base = st * kSubTokens;
+      if (PAGED && PAGE_UNIFORM && tok_base + kSubTokens <= n_b) {
+        const int in_page = tok_base & (a.page_size - 1);  // PAGE_UNIFORM: power-of-two page
+        const char* row0 = a.kv + (int64_t)page * a.kv_s0 + (int64_t)in_page * a.kv_s1;
+#pragma unroll
+        for (int ri = 0; ri < RG_PER_WAVE; ++ri) src[ri] = row0 + lane_row_off[ri];
+        return;
+      }
 #pragma unroll
       for (int ri = 0; ri < RG_PER_WAVE; ++ri) {
         const int rg = wave * RG_PER_WAVE + ri;
@@ -576,19 +597,25 @@ void mla_partial_kernel(PartialArgs a) {
         src[ri] = a.kv + row_offset<PAGED>(a, b, tok, n_b, pg) + ((lane & 7) ^ piece_swizzle(dma_r, rg)) * 16;
       }
     };
-    auto copy_one = [&](int st, int ri, auto CB, const char* const (&src)[RG_PER_WAVE]) __attribute__((always_inline)) {
+    // voff / roff: byte offsets of the destination entries in the V and rope
+    // rings (computed once per sub-tile, uniform)
+    auto copy_one = [&](int voff, int roff, int ri, auto CB, const char* const (&src)[RG_PER_WAVE])
+                        __attribute__((always_inline)) {
       constexpr int cb = decltype(CB)::value;
       const int rg = wave * RG_PER_WAVE + ri;
-      char LDS_AS* dst = cb < NVB ? lds + (st - st0) % kStages * VSLOT + (rg * NVB + cb) * 1024
-                                  : lds + OFF_R + (st - st0) % kRopeStages * RSLOT + (rg * NRB + cb - NVB) * 1024;
+      char LDS_AS* dst = cb < NVB ? lds + voff + (rg * NVB + cb) * 1024
+                                  : lds + OFF_R + roff + (rg * NRB + cb - NVB) * 1024;
       lds_copy16<cb * 128>(src[ri], dst);
     };
     auto issue = [&](int st, int page) __attribute__((always_inline)) {
       const char* src[RG_PER_WAVE];
       copy_src(st, page, src);
+      const int k = st - st0;  // >= 0
 #pragma unroll
       for (int ri = 0; ri < RG_PER_WAVE; ++ri)
-        static_for<NCB>([&](auto CB) __attribute__((always_inline)) { copy_one(st, ri, CB, src); });
+        static_for<NCB>([&](auto CB) __attribute__((always_inline)) {
+          copy_one(k % kStages * VSLOT, k % kRopeStages * RSLOT, ri, CB, src);
+        });
     };
 
     // One pass over a sub-tile pair: S^T of the sub-tile in kst (DO_S) and
@@ -745,17 +772,22 @@ void mla_partial_kernel(PartialArgs a) {
     // are in flight. One instance of the passes serves every iteration: at
     // i = -1 the PV half multiplies sub-tile 0 by P = 0 and adds exactly
     // nothing; at i = nst-1 the S half reads a stale entry and its result is
-    // discarded.
-    for (int i = -1; i < nst; ++i) {
+    // discarded. The body is instantiated twice: with the copies of sub-tile
+    // i+3 (every iteration with i + 3 < nst, no per-copy condition) and
+    // without them (the last three iterations).
+    static_assert(kStages == 4 && kRopeStages == 3, "ring offsets below");
+    auto iteration = [&](const int i, auto DOCOPY) __attribute__((always_inline)) {
+      constexpr bool do_copy = decltype(DOCOPY)::value;  // sub-tile i+3
       // sub-tile i+1 must have landed; sub-tile i+2 may still be in flight
-      if (i >= 0 && i + 1 < nst) {
+      if (do_copy) {  // here i + 2 < nst
+        if (i >= 0) wait_vmcnt<LOADS>();
+      } else if (i >= 0 && i + 1 < nst) {
         if (i + 2 < nst) {
           wait_vmcnt<LOADS>();
         } else {
           wait_vmcnt<0>();
         }
       }
-      const bool do_copy = i + kStages - 1 < nst;  // sub-tile i+3
       const int page = (PAGED && PAGE_UNIFORM && do_copy) ? page_ready(next_page) : 0;
       // every wave's P^T(i) and factors are written and every wave is done
       // with the ring entries refilled during this iteration
@@ -767,9 +799,15 @@ void mla_partial_kernel(PartialArgs a) {
         next_page = i < 0 ? pro_page[kStages - 1] : page_fetch(st0 + i + kStages);
       const int pbuf = i & 1;
       f32x4 alpha4 = ds_read_f32x4(lds + OFF_A + pbuf * ASLOT + (lane & 31) * 16);
-      const char LDS_AS* vst = lds + (i < 0 ? 0 : i % kStages) * VSLOT;
-      const char LDS_AS* kst_v = lds + (i + 1) % kStages * VSLOT;
-      const char LDS_AS* kst_r = lds + (i + 1) % kRopeStages * RSLOT;
+      // ring entries (i + 1 >= 0): S(i+1) reads entry i+1, PV(i) entry i
+      // (entry 0 at i = -1, where P = 0), the copies fill entry i+3
+      const unsigned k1 = (unsigned)(i + 1);
+      const unsigned r1 = k1 % 3u;
+      const char LDS_AS* vst = lds + (i < 0 ? 0u : (k1 + 3u) & 3u) * VSLOT;
+      const char LDS_AS* kst_v = lds + (k1 & 3u) * VSLOT;
+      const char LDS_AS* kst_r = lds + r1 * RSLOT;
+      const int copy_voff = (int)((k1 + 2u) & 3u) * VSLOT;
+      const int copy_roff = (int)(r1 == 0u ? 2u : r1 - 1u) * RSLOT;
       const char LDS_AS* pst = lds + OFF_P + pbuf * PSLOT;
       const int st_s = st0 + i + 1;  // sub-tile of this iteration's S
 
@@ -783,9 +821,7 @@ void mla_partial_kernel(PartialArgs a) {
         return [&](auto J) __attribute__((always_inline)) {
           constexpr int j = decltype(J)::value;
           constexpr int NST = decltype(NSTEPSC)::value;
-          if constexpr (j == 0) {
-            if (do_copy) copy_src(st0 + i + kStages - 1, page, csrc);
-          }
+          if constexpr (j == 0 && do_copy) copy_src(st0 + i + kStages - 1, page, csrc);
           if constexpr (j == PV_START - 1) {
             pin_f4(alpha4);
             bool any = false;
@@ -795,9 +831,8 @@ void mla_partial_kernel(PartialArgs a) {
           }
           static_for<LOADS>([&](auto K) __attribute__((always_inline)) {
             constexpr int k = decltype(K)::value;
-            if constexpr (k * NST / LOADS == j) {
-              if (do_copy) copy_one(st0 + i + kStages - 1, k / NCB, std::integral_constant<int, k % NCB>{}, csrc);
-            }
+            if constexpr (do_copy && k * NST / LOADS == j)
+              copy_one(copy_voff, copy_roff, k / NCB, std::integral_constant<int, k % NCB>{}, csrc);
           });
 
         };
@@ -895,7 +930,10 @@ void mla_partial_kernel(PartialArgs a) {
         else
           pv_iteration();
       }
-    }
+    };
+    int i = -1;
+    for (; i + kStages - 1 < nst; ++i) iteration(i, std::true_type{});
+    for (; i < nst; ++i) iteration(i, std::false_type{});
     // all waves must be done with the rings before they are reused below
     lds_barrier();
 
@@ -1202,6 +1240,7 @@ int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_
   a.kv_s0 = kv_stride_0 * 2;
   a.kv_s1 = kv_stride_1 * 2;
   a.num_blocks = num_blocks;
+  a.max_page = (int32_t)(num_blocks - 1 < INT32_MAX ? num_blocks - 1 : INT32_MAX);
   a.page_size = page_size;
   a.page_shift = (page_size & (page_size - 1)) == 0 ? __builtin_ctz((unsigned)page_size) : -1;
   a.bt = block_table;
@@ -1232,8 +1271,9 @@ int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_
   const int heads_per_wg = 32 * nhb;
   const int workers = num_splits > 0 ? batch * num_splits : num_workers;
   dim3 grid(workers, (num_heads + heads_per_wg - 1) / heads_per_wg);
-  // one page per 32-token sub-tile: sub-tiles never straddle a page
-  const bool uni = paged && (page_size % kSubTokens == 0);
+  // one page per 32-token sub-tile (sub-tiles never straddle a page) and a
+  // power-of-two page size: page slots and in-page rows by shifts and masks
+  const bool uni = paged && (page_size % kSubTokens == 0) && a.page_shift >= 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = dtype == TMLA_BF16 ? launch_partial_dt<TMLA_BF16>(a, grid, nhb, s, paged, uni)
                                     : launch_partial_dt<TMLA_FP16>(a, grid, nhb, s, paged, uni);
