@@ -119,6 +119,69 @@ int tmla_mla_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
 /* Number of compute units of `device` (0 on error); the default worker count. */
 int32_t tmla_device_cu_count(int32_t device);
 
+/*
+ * MLA layer glue: the absorbed-projection steps on either side of
+ * tmla_mla_decode in one decode step of the DeepSeek MLA layer. The dense
+ * projections (wq_a, wq_b, wkv_a, wo) stay library GEMMs. wkv_b is the
+ * layer's [num_heads * (qk_nope_dim + v_head_dim), kv_lora_rank] weight with
+ * row stride wkv_b_stride_0: rows h*(nope+v) .. +nope are W_UK[h], the next v
+ * rows W_UV[h] (the reference's view, src/triton_mla/model.py:96-99).
+ */
+
+/*
+ * Query side of the absorbed step: for every (b, h)
+ *   q_out[b, h, :rank]  = q_proj[b, h*(nope+rope) : +nope] . W_UK[h]
+ *   q_out[b, h, rank:]  = RoPE(q_proj[b, h*(nope+rope)+nope : +rope], positions[b])
+ * Replaces the q_pe RoPE of `MLA._project` (src/triton_mla/model.py:74-83,
+ * apply_rope model.py:44-50: rotate-half, theta ** (2i/rope), float32) and the
+ * W_UK einsum + concatenation of `MLA.forward` (model.py:108-109).
+ * q_proj is wq_b's output [batch, num_heads*(nope+rope)] (row stride
+ * q_proj_stride_b); q_out [batch, num_heads, rank+rope] with element strides
+ * (q_out_stride_b, q_out_stride_h, 1). Built for qk_nope_dim 128,
+ * qk_rope_dim 64 and kv_lora_rank a multiple of 256.
+ */
+int tmla_mla_absorb_q(const void* q_proj, int64_t q_proj_stride_b, const void* wkv_b,
+                      int64_t wkv_b_stride_0, const int32_t* positions, int32_t batch,
+                      int32_t num_heads, int32_t qk_nope_dim, int32_t qk_rope_dim,
+                      int32_t kv_lora_rank, int32_t v_head_dim, float rope_theta, int32_t dtype,
+                      void* q_out, int64_t q_out_stride_b, int64_t q_out_stride_h, void* stream);
+
+/*
+ * Output side of the absorbed step:
+ *   out[b, h*v_head_dim + v] = o_latent[b, h, :] . W_UV[h][v, :]
+ * Replaces the W_UV einsum of `MLA.forward` (src/triton_mla/model.py:120-124);
+ * out [batch, num_heads*v_head_dim] (row stride out_stride_b) is the input of
+ * the wo projection. o_latent is mla_decode's output [batch, num_heads,
+ * kv_lora_rank], element strides (o_stride_b, o_stride_h, 1). Built for
+ * v_head_dim 128 and kv_lora_rank a multiple of 128.
+ */
+int tmla_mla_absorb_out(const void* o_latent, int64_t o_stride_b, int64_t o_stride_h,
+                        const void* wkv_b, int64_t wkv_b_stride_0, int32_t batch,
+                        int32_t num_heads, int32_t qk_nope_dim, int32_t kv_lora_rank,
+                        int32_t v_head_dim, int32_t dtype, void* out, int64_t out_stride_b,
+                        void* stream);
+
+/*
+ * Cache append of the new token: for every sequence b
+ *   row = [RMSNorm(kv_proj[b, :rank]) * norm_weight, RoPE(kv_proj[b, rank:rank+rope])]
+ * written at position positions[b] (= cache_seqlens before the step) of
+ * sequence b: page block_table[b, pos / page_size], row pos % page_size, or
+ * row pos of sequence b when block_table is NULL (dense [batch, capacity, D],
+ * page_size 1, num_blocks = capacity). Replaces the kv half of `MLA._project`
+ * (src/triton_mla/model.py:80-83; RMSNorm model.py:34-41) and
+ * `MLA._append_kv` (model.py:86-94). RMSNorm in float32 (normalised value
+ * times the weight, rounded once to the cache dtype). A position
+ * whose page slot or page id lies outside the table or the cache is not
+ * written. norm_weight may be NULL (weight 1). Built for rope_dim 64 and
+ * kv_lora_rank a multiple of 64 up to 1024.
+ */
+int tmla_mla_kv_append(const void* kv_proj, int64_t kv_proj_stride_b, const void* norm_weight,
+                       float eps, float rope_theta, const int32_t* positions, int32_t batch,
+                       int32_t kv_lora_rank, int32_t rope_dim, int32_t dtype, void* kv_cache,
+                       int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks,
+                       int32_t page_size, const int32_t* block_table, int64_t bt_stride_b,
+                       int32_t bt_cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

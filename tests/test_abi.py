@@ -74,3 +74,37 @@ def test_invalid_arguments_rejected_on_host(lib):
     # null tensors are caught before any launch
     assert _partial(lib, ws=fake, wsb=ws) == 1
     assert b"null" in lib.tmla_last_error()
+
+
+def test_layer_glue_arguments_rejected_on_host(lib):
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    # tmla_mla_absorb_q(q_proj, q_sb, wkv_b, w_s0, positions, batch, heads, nope, rope, rank, vd, theta,
+    #                   dtype, q_out, qo_sb, qo_sh, stream)
+    q = [fake, 128 * 192, fake, 512, fake, 2, 128, 128, 64, 512, 128, 1e4, 0, fake, 128 * 576, 576, None]
+    args = list(q); args[12] = 5
+    assert lib.tmla_mla_absorb_q(*args) == 1 and b"dtype" in lib.tmla_last_error()
+    args = list(q); args[7] = 96
+    assert lib.tmla_mla_absorb_q(*args) == 2  # qk_nope_dim other than 128
+    args = list(q); args[9] = 384
+    assert lib.tmla_mla_absorb_q(*args) == 2  # rank not a multiple of 256
+    args = list(q); args[0] = None
+    assert lib.tmla_mla_absorb_q(*args) == 1 and b"null" in lib.tmla_last_error()
+    args = list(q); args[1] = 128 * 192 + 3
+    assert lib.tmla_mla_absorb_q(*args) == 1  # stride not a multiple of 8 elements
+    args = list(q); args[5] = 0
+    assert lib.tmla_mla_absorb_q(*args) == 0  # empty batch: nothing to do
+    # tmla_mla_absorb_out(o, o_sb, o_sh, wkv_b, w_s0, batch, heads, nope, rank, vd, dtype, out, out_sb, stream)
+    o = [fake, 128 * 512, 512, fake, 512, 2, 128, 128, 512, 128, 0, fake, 128 * 128, None]
+    args = list(o); args[9] = 64
+    assert lib.tmla_mla_absorb_out(*args) == 2  # v_head_dim other than 128
+    args = list(o); args[11] = None
+    assert lib.tmla_mla_absorb_out(*args) == 1
+    # tmla_mla_kv_append(kv_proj, sb, norm_w, eps, theta, positions, batch, rank, rope, dtype, cache, s0, s1,
+    #                    num_blocks, page_size, bt, bt_sb, bt_cols, stream)
+    k = [fake, 576, None, 1e-6, 1e4, fake, 2, 512, 64, 0, fake, 64 * 576, 576, 4, 64, fake, 4, 4, None]
+    args = list(k); args[8] = 32
+    assert lib.tmla_mla_kv_append(*args) == 2  # rope_dim other than 64
+    args = list(k); args[15] = None  # dense cache needs page_size 1
+    assert lib.tmla_mla_kv_append(*args) == 1 and b"page_size" in lib.tmla_last_error()
+    args = list(k); args[13] = 0
+    assert lib.tmla_mla_kv_append(*args) == 1

@@ -1,0 +1,193 @@
+"""HIP glue of the absorbed MLA decode step (triton_mla.layer_ops) against the
+float64 oracle restatement of the reference layer (oracle/oracle.py:
+rms_norm, apply_rope, the W_UK / W_UV einsums; src/triton_mla/model.py:34-50,
+74-124).
+
+The kernels compute in float32 from bf16 inputs and round once to bf16, as
+the reference's float32 torch steps do. Each output element must lie within
+half a bf16 ulp of the float64 value plus the float32 error bound of its
+computation (n * 2^-24 * sum |a_i b_i| for an n-term dot product; the float32
+angle error (|angle| + 2) * 2^-22 times |x1| + |x2| for a rotation), and at
+least 99.9% of the elements must equal the correctly rounded bf16 of the
+float64 value. The cache append must leave every other cache row untouched,
+bit for bit; RoPE is also compared with the reference's torch apply_rope run
+on the GPU in float32 (within one bf16 ulp plus twice the float32 bound).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import bits
+
+pytestmark = pytest.mark.gpu
+
+ROPE_THETA = 10000.0
+
+
+def ulp_bf16(x):
+    """Spacing of bf16 numbers around |x| (float64)."""
+    ax = np.maximum(np.abs(x), 2.0 ** -126)
+    return 2.0 ** (np.floor(np.log2(ax)) - 7)
+
+
+def assert_matches(got_bits, ref64, f32_bound, what, min_exact=0.999):
+    """|got - ref| <= ulp/2 + f32_bound elementwise; most elements correctly rounded."""
+    got = oracle.half_to_float(got_bits, "bf16")
+    err = np.abs(got - ref64)
+    bound = 0.5 * ulp_bf16(ref64) + f32_bound
+    worst = float(np.max(err / bound))
+    exact = float(np.mean(got_bits == oracle.float_to_half(ref64, "bf16")))
+    print(f"{what}: max err / bound {worst:.3f}, correctly rounded {exact:.5f}", flush=True)
+    assert worst <= 1.0, f"{what}: error above the float32 + rounding bound ({worst})"
+    assert exact >= min_exact, f"{what}: only {exact:.4f} of the elements correctly rounded"
+
+
+def dot_bound(n, abs_products_sum):
+    """Float32 accumulation error bound of an n-term sum of products."""
+    return n * 2.0 ** -24 * abs_products_sum
+
+
+def rope_bound(x, positions, theta):
+    """Float32 error of a rotation: the angle pos / theta^(2i/d) carries a
+    relative error of a few 2^-24, times |x1| + |x2|."""
+    d = x.shape[-1]
+    freq = theta ** (np.arange(0, d, 2) / d)
+    ang = np.asarray(positions, dtype=np.float64)[..., None] / freq
+    mag = np.abs(x[..., : d // 2]) + np.abs(x[..., d // 2:])
+    b = mag * (np.abs(ang) + 2.0) * 2.0 ** -22
+    return np.concatenate([b, b], axis=-1)
+
+
+def f64(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("layout", ["paged16", "paged64", "dense"])
+def test_kv_append_matches_oracle(gpu, layout):
+    from triton_mla import layer_ops
+
+    gen = torch.Generator().manual_seed(11)
+    rank, rope, eps = 512, 64, 1e-6
+    positions = torch.tensor([0, 15, 16, 63, 64, 200, 511], dtype=torch.int32)
+    batch = positions.shape[0]
+    kv_proj = torch.randn(batch, rank + rope, generator=gen).to(torch.bfloat16)
+    weight = (1.0 + 0.3 * torch.randn(rank, generator=gen)).to(torch.bfloat16)
+    if layout == "dense":
+        cache = torch.randn(batch, 512, rank + rope, generator=gen).to(torch.bfloat16)
+        bt = None
+    else:
+        page = 16 if layout == "paged16" else 64
+        pages = 512 // page
+        cache = torch.randn(batch * pages, page, rank + rope, generator=gen).to(torch.bfloat16)
+        bt = torch.randperm(batch * pages, generator=gen).view(batch, pages).int()
+    before = cache.clone()
+    gcache = cache.to(gpu)
+    layer_ops.kv_append(kv_proj.to(gpu), weight.to(gpu), eps, ROPE_THETA, positions.to(gpu), gcache,
+                        None if bt is None else bt.to(gpu), rank, rope)
+    torch.cuda.synchronize(gpu)
+    after = gcache.cpu()
+
+    pos = positions.long()
+    if bt is None:
+        rows = (torch.arange(batch), pos)
+    else:
+        page = cache.shape[1]
+        rows = (bt[torch.arange(batch), pos // page].long(), pos % page)
+    got = bits(after[rows])
+    x = f64(kv_proj)
+    ref = np.concatenate([oracle.rms_norm(x[:, :rank], f64(weight), eps),
+                          oracle.apply_rope(x[:, rank:], positions.numpy(), ROPE_THETA)], axis=-1)
+    w = f64(weight)
+    norm_bound = (rank + 8) * 2.0 ** -24 * np.abs(ref[:, :rank])  # mean of squares, rsqrt, two products
+    bound = np.concatenate([norm_bound, rope_bound(x[:, rank:], positions.numpy(), ROPE_THETA)], axis=-1)
+    assert_matches(got, ref, bound, f"appended rows ({layout})")
+    mask = torch.ones(after.shape[:2], dtype=torch.bool)
+    mask[rows] = False
+    assert np.array_equal(bits(after[mask]), bits(before[mask])), "rows other than the appended ones changed"
+
+
+@pytest.mark.parametrize("batch,heads", [(1, 16), (16, 128), (33, 16)])
+def test_absorb_q_matches_oracle(gpu, batch, heads):
+    from triton_mla import layer_ops
+
+    gen = torch.Generator().manual_seed(12 + batch)
+    nope, rope, rank, vd = 128, 64, 512, 128
+    q_proj = torch.randn(batch, heads * (nope + rope), generator=gen).to(torch.bfloat16)
+    wkv_b = (0.05 * torch.randn(heads * (nope + vd), rank, generator=gen)).to(torch.bfloat16)
+    positions = torch.randint(0, 20000, (batch,), generator=gen, dtype=torch.int32)
+    out = layer_ops.absorb_q(q_proj.to(gpu), wkv_b.to(gpu), positions.to(gpu), heads, nope, rope, rank, vd,
+                             ROPE_THETA)
+    torch.cuda.synchronize(gpu)
+    assert out.shape == (batch, heads, rank + rope)
+    q = f64(q_proj).reshape(batch, heads, nope + rope)
+    w = {"wkv_b": f64(wkv_b)}
+    cfg = {"num_heads": heads, "qk_nope_head_dim": nope, "v_head_dim": vd, "kv_lora_rank": rank}
+    q_pe = oracle.apply_rope(q[..., nope:], positions.numpy()[:, None], ROPE_THETA)
+    ref = oracle.layer_absorbed_query(w, cfg, q[..., :nope], q_pe)
+    got = bits(out.cpu())
+    w_uk = f64(wkv_b).reshape(heads, nope + vd, rank)[:, :nope]
+    abs_sum = np.einsum("bhd,hdc->bhc", np.abs(q[..., :nope]), np.abs(w_uk))
+    assert_matches(got[..., :rank], ref[..., :rank], dot_bound(nope, abs_sum), f"q_nope . W_UK (B={batch}, H={heads})")
+    # positions up to 20000: the float32 angle (as in the reference's float32
+    # apply_rope) moves about 2% of the results off the float64 rounding
+    assert_matches(got[..., rank:], ref[..., rank:], rope_bound(q[..., nope:], positions.numpy()[:, None], ROPE_THETA),
+                   f"RoPE(q_pe) (B={batch}, H={heads})", min_exact=0.95)
+    # the reference's own float32 rotation on the GPU
+    from triton_mla.model import apply_rope
+
+    q_pe_dev = q_proj.to(gpu).view(batch, heads, nope + rope)[..., nope:]
+    torch_rope = apply_rope(q_pe_dev, positions.to(gpu)[:, None], ROPE_THETA).float().cpu()
+    # two float32 evaluations: each within rope_bound of float64
+    tol = ulp_bf16(torch_rope.numpy().astype(np.float64)) + 2 * rope_bound(q[..., nope:], positions.numpy()[:, None],
+                                                                           ROPE_THETA)
+    diff = (out[..., rank:].float().cpu() - torch_rope).abs().numpy()
+    assert bool((diff <= tol).all()), f"RoPE differs from torch's float32 rotation by {float(np.max(diff / tol))} x tol"
+
+
+@pytest.mark.parametrize("batch,heads", [(1, 16), (16, 128), (40, 16)])
+def test_absorb_out_matches_oracle(gpu, batch, heads):
+    from triton_mla import layer_ops
+
+    gen = torch.Generator().manual_seed(13 + batch)
+    nope, rank, vd = 128, 512, 128
+    o_lat = torch.randn(batch, heads, rank, generator=gen).to(torch.bfloat16)
+    wkv_b = (0.05 * torch.randn(heads * (nope + vd), rank, generator=gen)).to(torch.bfloat16)
+    out = layer_ops.absorb_out(o_lat.to(gpu), wkv_b.to(gpu), heads, nope, rank, vd)
+    torch.cuda.synchronize(gpu)
+    assert out.shape == (batch, heads * vd)
+    w_uv = f64(wkv_b).reshape(heads, nope + vd, rank)[:, nope:]
+    ref = np.einsum("bhc,hdc->bhd", f64(o_lat), w_uv).reshape(batch, heads * vd)
+    abs_sum = np.einsum("bhc,hdc->bhd", np.abs(f64(o_lat)), np.abs(w_uv)).reshape(batch, heads * vd)
+    assert_matches(bits(out.cpu()), ref, dot_bound(rank, abs_sum), f"o . W_UV (B={batch}, H={heads})")
+
+
+def test_hip_glue_matches_torch_glue(gpu):
+    """The absorbed step with the HIP glue and with the reference's torch glue
+    (same mla_decode inside) on the same inputs: the appended rows agree to
+    one bf16 ulp and the layer outputs to the bf16 GEMM tolerance."""
+    from triton_mla import MLA, MLAConfig
+
+    gen = torch.Generator().manual_seed(14)
+    cfg = MLAConfig(hidden_size=512, num_heads=32, q_lora_rank=256)
+    model = MLA(cfg)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_(torch.randn(p.shape, generator=gen) * 0.05)
+        model.kv_norm.weight.copy_(1.0 + 0.2 * torch.randn(cfg.kv_lora_rank, generator=gen))
+    model = model.to(gpu, torch.bfloat16)
+    batch, page, pages = 5, 64, 8
+    seqlens = torch.tensor([0, 1, 63, 64, 300], dtype=torch.int32, device=gpu)
+    bt = torch.randperm(batch * pages, generator=gen).view(batch, pages).int().to(gpu)
+    cache = torch.randn(batch * pages, page, cfg.kv_cache_dim, generator=gen).to(gpu, torch.bfloat16)
+    x = torch.randn(batch, cfg.hidden_size, generator=gen).to(gpu, torch.bfloat16)
+    ca, cb = cache.clone(), cache.clone()
+    with torch.no_grad():
+        out_hip, lens_hip = model(x, ca, seqlens, bt)
+        out_torch, lens_torch = model.forward_torch_glue(x, cb, seqlens, bt)
+    assert torch.equal(lens_hip, lens_torch)
+    diff = (ca.float() - cb.float()).abs()
+    ulp = torch.from_numpy(ulp_bf16(cb.float().cpu().numpy().astype(np.float64))).to(gpu)
+    assert bool((diff <= ulp).all()), "appended rows differ by more than one bf16 ulp"
+    torch.testing.assert_close(out_hip.float(), out_torch.float(), atol=3e-2, rtol=3e-2)

@@ -48,7 +48,11 @@ def test_absorbed_decode_matches_naive(gpu, paged):
         out, new_lens = model(x, cache_a, seqlens, block_table)
         ref, _ = model.forward_naive(x, cache_b, seqlens, block_table)
     assert torch.equal(new_lens, seqlens + 1)
-    assert torch.equal(cache_a, cache_b)  # both paths append the same row
+    # both paths append the same row: the HIP append (forward) and the torch
+    # one (forward_naive) round float32 results once, so they agree to one
+    # bf16 ulp; every other cache row is untouched by both
+    spacing = torch.exp2(torch.floor(torch.log2(cache_b.float().abs().clamp_min(2.0 ** -126))) - 7)
+    assert bool(((cache_a.float() - cache_b.float()).abs() <= spacing).all())
     torch.testing.assert_close(out.float(), ref.float(), atol=3e-2, rtol=3e-2)
 
 

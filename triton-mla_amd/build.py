@@ -20,7 +20,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "triton_mla", "libtriton_mla_hip.so")
-SOURCES = ["mla_decode.hip"]
+SOURCES = ["mla_decode.hip", "mla_layer.hip"]
 ARCH = os.environ.get("TRITON_MLA_ARCH", "gfx950")
 
 

@@ -32,6 +32,13 @@ SIGNATURES = {
     "tmla_mla_decode": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
         _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "tmla_mla_absorb_q": (ctypes.c_int, [
+        _vp, _i64, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp, _i64, _i64, _vp]),
+    "tmla_mla_absorb_out": (ctypes.c_int, [
+        _vp, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp]),
+    "tmla_mla_kv_append": (ctypes.c_int, [
+        _vp, _i64, _vp, _f32, _f32, _vp, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32,
+        _vp]),
 }
 
 STATUS = {0: "TMLA_OK", 1: "TMLA_ERR_INVALID_ARGUMENT", 2: "TMLA_ERR_UNSUPPORTED",

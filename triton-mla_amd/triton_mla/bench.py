@@ -9,7 +9,11 @@ Same command line and CSV columns as the reference's benchmark
 column keeps its name for drop-in CSV consumers and holds the HIP kernels'
 time; ``config`` names the launch shape that ran. Additions: --workload runs
 the named seeded workloads of triton_mla.workloads (uniform and ragged
-lengths), --splits picks the split scheme, --no-compile skips torch.compile.
+lengths), --splits picks the split scheme, --no-compile skips torch.compile,
+--layer times one decode step of the whole MLA layer at DeepSeek-V3 dims
+(random N(0, 0.02) bf16 weights, --batch sequences of --seqlen cached tokens)
+with the HIP glue (MLA.forward) and with the reference's torch glue
+(MLA.forward_torch_glue) around the same mla_decode.
 
 Timing: median of --reps runs, each preceded by a 512 MiB read that evicts
 the Infinity Cache, bracketed by HIP events on the current stream (the
@@ -96,6 +100,48 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
                          "eager_us": t_eager, "compile_us": t_compile})
 
 
+def bench_layer(args, device, flush):
+    """One MLA decode step at DeepSeek-V3 dims: HIP glue vs torch glue."""
+    from .model import MLA, MLAConfig
+
+    cfg = MLAConfig()
+    gen = torch.Generator().manual_seed(0)
+    model = MLA(cfg)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if "norm" not in name:
+                p.copy_(torch.randn(p.shape, generator=gen) * 0.02)
+    model = model.to(device, DTYPES[args.dtype])
+    weight_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    print(f"# MLA layer step, DeepSeek-V3 dims, weights {weight_bytes / 1e6:.1f} MB, {args.dtype}")
+    print("| batch | context | hip glue us | torch glue us | mla_decode us | glue saved us | layer roofline us |")
+    print("|---|---|---|---|---|---|---|")
+    for batch in args.batch:
+        for ctx in args.seqlen:
+            page = args.page_size
+            pages = -(-(ctx + 1) // page)
+            cache = torch.randn(batch * pages, page, cfg.kv_cache_dim, generator=gen).to(device, model.wq_a.weight.dtype)
+            bt = torch.randperm(batch * pages, generator=gen).view(batch, pages).int().to(device)
+            seqlens = torch.full((batch,), ctx, dtype=torch.int32, device=device)
+            x = torch.randn(batch, cfg.hidden_size, generator=gen).to(device, cache.dtype)
+            with torch.no_grad():
+                out_h, _ = model(x, cache, seqlens, bt)
+                out_t, _ = model.forward_torch_glue(x, cache, seqlens, bt)
+                torch.testing.assert_close(out_h.float(), out_t.float(), atol=3e-2, rtol=3e-2)
+                t_h = time_us(lambda: model(x, cache, seqlens, bt), reps=args.reps, flush=flush, device=device)
+                t_t = time_us(lambda: model.forward_torch_glue(x, cache, seqlens, bt), reps=args.reps, flush=flush,
+                              device=device)
+                q = torch.randn(batch, cfg.num_heads, cfg.kv_cache_dim, generator=gen).to(device, cache.dtype)
+                call = DecodeLaunch(q, cache, seqlens + 1, bt, cfg.kv_lora_rank, cfg.qk_head_dim ** -0.5, None)
+                t_d = time_us(call.run, reps=args.reps, flush=flush, device=device)
+            kv_bytes = batch * (ctx + 1) * cfg.kv_cache_dim * cache.element_size()
+            roof = (weight_bytes + kv_bytes) / 8.0e12 * 1e6
+            print(f"| {batch} | {ctx} | {t_h['median']:.1f} | {t_t['median']:.1f} | {t_d['median']:.1f} | "
+                  f"{t_t['median'] - t_h['median']:.1f} | {roof:.1f} |", flush=True)
+            del cache, bt, x, q, call
+            torch.cuda.empty_cache()
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--batch", type=int, nargs="+", default=[1, 8, 32, 64, 128])
@@ -111,11 +157,16 @@ def main(argv=None):
                         help="run these named workloads instead of the --batch x --seqlen grid")
     parser.add_argument("--splits", default="balanced", help="'balanced' or a per-sequence split count")
     parser.add_argument("--reps", type=int, default=100)
+    parser.add_argument("--layer", action="store_true",
+                        help="time the MLA layer step at DeepSeek-V3 dims (HIP glue vs torch glue)")
     args = parser.parse_args(argv)
 
     device = torch.device("cuda")
     dtype = DTYPES[args.dtype]
     flush = Flusher(device)
+    if args.layer:
+        bench_layer(args, device, flush)
+        return
     compiled = None
     if not args.no_compile:
         compiled = torch.compile(mla_decode_torch, mode=args.compile_mode, dynamic=False)

@@ -5,8 +5,13 @@ Same module structure, parameter names and math as the reference layer
 ``MLAConfig`` (model.py:13-31), ``RMSNorm`` (model.py:34-41), rotate-half
 ``apply_rope`` (model.py:44-50) and ``MLA`` with ``forward`` (absorbed:
 W_UK folded into the query, W_UV applied after attention, model.py:101-124)
-and ``forward_naive`` (decompressed per-head K/V, model.py:126-144). The
-attention of ``forward`` is the HIP ``mla_decode``.
+and ``forward_naive`` (decompressed per-head K/V, model.py:126-144). In
+``forward`` the attention is the HIP ``mla_decode`` and the glue around it
+runs as HIP kernels too (triton_mla.layer_ops): the cache append (RMSNorm of
+the latent, RoPE of the key, paged write), the W_UK absorption with the q_pe
+RoPE, and the W_UV product; the dense projections stay library GEMMs.
+``forward_naive`` keeps the reference's torch steps: it is the layer's
+oracle.
 """
 
 from __future__ import annotations
@@ -17,6 +22,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import layer_ops
 from .kernel import mla_decode
 from .reference import gather_kv
 
@@ -115,6 +121,29 @@ class MLA(nn.Module):
         Appends the new token to kv_cache in place and returns
         (output [batch, hidden], updated cache_seqlens).
         """
+        cfg = self.cfg
+        if kv_cache.dtype != x.dtype:
+            raise NotImplementedError("MLA.forward needs the cache in the layer's dtype")
+        q_proj = self.wq_b(self.q_norm(self.wq_a(x)))  # [B, H * (nope + rope)]
+        kv_proj = self.wkv_a(x)  # [B, rank + rope]
+        # RMSNorm(c_kv), RoPE(k_pe) and the paged append (model.py:80-94)
+        layer_ops.kv_append(kv_proj, self.kv_norm.weight, self.kv_norm.eps, cfg.rope_theta, cache_seqlens,
+                            kv_cache, block_table, cfg.kv_lora_rank, cfg.qk_rope_head_dim)
+        seqlens = cache_seqlens + 1
+        # q = [q_nope . W_UK, RoPE(q_pe)] (model.py:74-79, 108-109)
+        q = layer_ops.absorb_q(q_proj, self.wkv_b.weight, cache_seqlens, cfg.num_heads, cfg.qk_nope_head_dim,
+                               cfg.qk_rope_head_dim, cfg.kv_lora_rank, cfg.v_head_dim, cfg.rope_theta)
+        o = mla_decode(q, kv_cache, seqlens, block_table, head_dim_v=cfg.kv_lora_rank,
+                       softmax_scale=self.softmax_scale, num_splits=num_splits)
+        # o . W_UV^T per head (model.py:120-124), then wo
+        o = layer_ops.absorb_out(o, self.wkv_b.weight, cfg.num_heads, cfg.qk_nope_head_dim, cfg.kv_lora_rank,
+                                 cfg.v_head_dim)
+        return self.wo(o), seqlens
+
+    def forward_torch_glue(self, x, kv_cache, cache_seqlens, block_table=None, num_splits=None):
+        """The absorbed step with the reference's torch glue around the HIP
+        mla_decode (model.py:101-124): the baseline the HIP glue is timed
+        against."""
         q_nope, q_pe, c_kv, k_pe = self._project(x, cache_seqlens)
         self._append_kv(kv_cache, c_kv, k_pe, cache_seqlens, block_table)
         seqlens = cache_seqlens + 1
