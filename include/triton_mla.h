@@ -138,7 +138,7 @@ int32_t tmla_device_cu_count(int32_t device);
  * q_proj is wq_b's output [batch, num_heads*(nope+rope)] (row stride
  * q_proj_stride_b); q_out [batch, num_heads, rank+rope] with element strides
  * (q_out_stride_b, q_out_stride_h, 1). Built for qk_nope_dim 128,
- * qk_rope_dim 64 and kv_lora_rank a multiple of 256.
+ * qk_rope_dim 64 and kv_lora_rank a multiple of 128.
  */
 int tmla_mla_absorb_q(const void* q_proj, int64_t q_proj_stride_b, const void* wkv_b,
                       int64_t wkv_b_stride_0, const int32_t* positions, int32_t batch,
@@ -153,7 +153,7 @@ int tmla_mla_absorb_q(const void* q_proj, int64_t q_proj_stride_b, const void* w
  * out [batch, num_heads*v_head_dim] (row stride out_stride_b) is the input of
  * the wo projection. o_latent is mla_decode's output [batch, num_heads,
  * kv_lora_rank], element strides (o_stride_b, o_stride_h, 1). Built for
- * v_head_dim 128 and kv_lora_rank a multiple of 128.
+ * v_head_dim a multiple of 32 and kv_lora_rank a multiple of 512.
  */
 int tmla_mla_absorb_out(const void* o_latent, int64_t o_stride_b, int64_t o_stride_h,
                         const void* wkv_b, int64_t wkv_b_stride_0, int32_t batch,

@@ -85,8 +85,8 @@ def test_layer_glue_arguments_rejected_on_host(lib):
     assert lib.tmla_mla_absorb_q(*args) == 1 and b"dtype" in lib.tmla_last_error()
     args = list(q); args[7] = 96
     assert lib.tmla_mla_absorb_q(*args) == 2  # qk_nope_dim other than 128
-    args = list(q); args[9] = 384
-    assert lib.tmla_mla_absorb_q(*args) == 2  # rank not a multiple of 256
+    args = list(q); args[9] = 320
+    assert lib.tmla_mla_absorb_q(*args) == 2  # rank not a multiple of 128
     args = list(q); args[0] = None
     assert lib.tmla_mla_absorb_q(*args) == 1 and b"null" in lib.tmla_last_error()
     args = list(q); args[1] = 128 * 192 + 3
@@ -95,8 +95,8 @@ def test_layer_glue_arguments_rejected_on_host(lib):
     assert lib.tmla_mla_absorb_q(*args) == 0  # empty batch: nothing to do
     # tmla_mla_absorb_out(o, o_sb, o_sh, wkv_b, w_s0, batch, heads, nope, rank, vd, dtype, out, out_sb, stream)
     o = [fake, 128 * 512, 512, fake, 512, 2, 128, 128, 512, 128, 0, fake, 128 * 128, None]
-    args = list(o); args[9] = 64
-    assert lib.tmla_mla_absorb_out(*args) == 2  # v_head_dim other than 128
+    args = list(o); args[9] = 48
+    assert lib.tmla_mla_absorb_out(*args) == 2  # v_head_dim not a multiple of 32
     args = list(o); args[11] = None
     assert lib.tmla_mla_absorb_out(*args) == 1
     # tmla_mla_kv_append(kv_proj, sb, norm_w, eps, theta, positions, batch, rank, rope, dtype, cache, s0, s1,

@@ -15,11 +15,11 @@
 //    ds_read_b64_tr_b16 as the A operand of v_mfma_f32_32x32x16; q_nope^T is
 //    the B operand, loaded from memory in the k order the transposed read
 //    produces. Output tile O^T = W_UK^T . q_nope^T, 32 columns x 32 batch rows
-//    per MFMA block.
+//    per MFMA block, one block per wave.
 //  * mla_absorb_out_kernel: o[b, h*vd + v] = o_lat[b, h] . W_UV[h][v] (the v
 //    rows of wkv_b, [vd, rank], rank contiguous): both MFMA operands are
 //    contiguous in the contraction index, so they are loaded straight from
-//    memory.
+//    memory; four waves split the contraction of each 32 x 32 block.
 //  * mla_kv_append_kernel: RMSNorm of the latent, RoPE of the key, and the
 //    new row written at position cache_seqlens[b] through the block table.
 #include <math.h>
@@ -34,7 +34,7 @@ namespace layer {
 
 constexpr int kNope = 128;   // qk_nope_head_dim the q kernel is built for
 constexpr int kRope = 64;    // qk_rope_head_dim
-constexpr int kColsWG = 256; // W_UK columns per workgroup (4 waves x 2 blocks of 32)
+constexpr int kColsWG = 128; // W_UK columns per workgroup (4 waves x 1 block of 32)
 constexpr int kBTile = 32;   // batch rows per MFMA block (N of the 32x32x16 MFMA)
 
 struct AbsorbQArgs {
@@ -94,7 +94,7 @@ __device__ __forceinline__ float ld(const short* p) {
 }
 
 // ---------------------------------------------------------------------------
-// q side: grid (heads, rank / 256, cdiv(batch, 32)), 4 waves
+// q side: grid (heads, rank / 128, cdiv(batch, 32)), 4 waves
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(256) void mla_absorb_q_kernel(AbsorbQArgs a) {
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void mla_absorb_q_kernel(AbsorbQArgs a) {
   constexpr int SUB = 32;                 // W rows per LDS sub-tile
   constexpr int SUBBYTES = SUB * kColsWG * 2;
   constexpr int NSUB = kNope / SUB;       // 4
-  __shared__ __attribute__((aligned(1024))) char smem[NSUB * SUBBYTES];  // 64 KiB
+  __shared__ __attribute__((aligned(1024))) char smem[NSUB * SUBBYTES];  // 32 KiB
   char LDS_AS* const lds = (char LDS_AS*)(void LDS_AS*)smem;
 
   const int lane = threadIdx.x & 63;
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void mla_absorb_q_kernel(AbsorbQArgs a) {
   const int col0 = blockIdx.y * kColsWG;
   const int b0 = blockIdx.z * kBTile;
 
-  // W_UK[h] rows [32*wave, 32*wave + 32), columns [col0, col0 + 256) into
+  // W_UK[h] rows [32*wave, 32*wave + 32), columns [col0, col0 + 128) into
   // sub-tile `wave`: block (rg, cb) holds rows 8rg..8rg+7 x 128 bytes, piece p
   // of row r at slot r*8 + (p ^ piece_swizzle(r, rg)).
   {
@@ -122,10 +122,10 @@ __global__ __launch_bounds__(256) void mla_absorb_q_kernel(AbsorbQArgs a) {
       const int64_t row = (int64_t)h * (kNope + a.vd) + SUB * wave + 8 * rg + r;
       const char* src = reinterpret_cast<const char*>(a.w + row * a.w_s0 + col0) + p * 16;
       char LDS_AS* dst = lds + wave * SUBBYTES + rg * NCB * 1024;
-      lds_copy16<0>(src, dst);
-      lds_copy16<128>(src, dst + 1024);
-      lds_copy16<256>(src, dst + 2048);
-      lds_copy16<384>(src, dst + 3072);
+      static_for<NCB>([&](auto CB) __attribute__((always_inline)) {
+        constexpr int cb = decltype(CB)::value;
+        lds_copy16<cb * 128>(src, dst + cb * 1024);
+      });
     }
   }
 
@@ -148,32 +148,28 @@ __global__ __launch_bounds__(256) void mla_absorb_q_kernel(AbsorbQArgs a) {
   wait_vmcnt<0>();
   lds_barrier();
 
-  // A operand W_UK^T: this wave's two 32-column blocks (128-byte column
-  // block `wave`, halves dbp = 0, 1); the addressing is that of the decode
-  // kernel's V^T operand with the row-group stride of this tile (NCB KiB).
+  // A operand W_UK^T: this wave's 32-column block (half dbp = wave & 1 of
+  // the 128-byte column block wave >> 1); the addressing is that of the
+  // decode kernel's V^T operand with the row-group stride of this tile
+  // (NCB KiB).
   const int g = lane >> 4, L = lane & 15;
   const int rr = 4 * (g >> 1) + (L >> 2);
-  const char LDS_AS* base[2][2];
+  const char LDS_AS* base[2];
 #pragma unroll
-  for (int dbp = 0; dbp < 2; ++dbp)
-#pragma unroll
-    for (int e2 = 0; e2 < 2; ++e2) {
-      const int piece = 4 * dbp + 2 * (g & 1) + ((L & 3) >> 1);
-      base[dbp][e2] = lds + e2 * NCB * 1024 + wave * 1024 + (rr * 8 + (piece ^ piece_swizzle(rr, e2))) * 16 +
-                      8 * (L & 1);
-    }
-  f32x16 acc[2] = {(f32x16)0.0f, (f32x16)0.0f};
+  for (int e2 = 0; e2 < 2; ++e2) {
+    const int piece = 4 * (wave & 1) + 2 * (g & 1) + ((L & 3) >> 1);
+    base[e2] = lds + e2 * NCB * 1024 + (wave >> 1) * 1024 + (rr * 8 + (piece ^ piece_swizzle(rr, e2))) * 16 +
+               8 * (L & 1);
+  }
+  f32x16 acc = (f32x16)0.0f;
   static_for<kNope / 16>([&](auto KK) __attribute__((always_inline)) {
     constexpr int kk = decltype(KK)::value;
     constexpr int st = kk / 2, c2 = kk % 2;
     constexpr int off = st * SUBBYTES + c2 * 2 * NCB * 1024;
-    i16x4 l0 = ds_read_tr<off>(base[0][0]), h0 = ds_read_tr<off>(base[0][1]);
-    i16x4 l1 = ds_read_tr<off>(base[1][0]), h1 = ds_read_tr<off>(base[1][1]);
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(l0), "+v"(h0), "+v"(l1), "+v"(h1));
+    i16x4 l0 = ds_read_tr<off>(base[0]), h0 = ds_read_tr<off>(base[1]);
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(l0), "+v"(h0));
     const i16x8 v0 = {l0[0], l0[1], l0[2], l0[3], h0[0], h0[1], h0[2], h0[3]};
-    const i16x8 v1 = {l1[0], l1[1], l1[2], l1[3], h1[0], h1[1], h1[2], h1[3]};
-    acc[0] = Elt<DT>::mfma(v0, qop[kk], acc[0]);
-    acc[1] = Elt<DT>::mfma(v1, qop[kk], acc[1]);
+    acc = Elt<DT>::mfma(v0, qop[kk], acc);
   });
 
   // D[m = column][n = batch row]: lane holds batch row b0 + lane%32 and
@@ -181,15 +177,13 @@ __global__ __launch_bounds__(256) void mla_absorb_q_kernel(AbsorbQArgs a) {
   if (brow_ok) {
     short* orow = a.out + (int64_t)(b0 + bl) * a.out_sb + (int64_t)h * a.out_sh;
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
+    for (int j = 0; j < 4; ++j) {
+      i16x4 v;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        i16x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = Elt<DT>::from_float(acc[jb][4 * j + e]);
-        const int c = col0 + 64 * wave + 32 * jb + 8 * j + 4 * hi;
-        *reinterpret_cast<i16x4*>(orow + c) = v;
-      }
+      for (int e = 0; e < 4; ++e) v[e] = Elt<DT>::from_float(acc[4 * j + e]);
+      const int c = col0 + 32 * wave + 8 * j + 4 * hi;
+      *reinterpret_cast<i16x4*>(orow + c) = v;
+    }
   }
 
   // RoPE of q_pe: the first column block of every batch tile; rows x pairs
@@ -209,23 +203,29 @@ __global__ __launch_bounds__(256) void mla_absorb_q_kernel(AbsorbQArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// output side: grid (heads, cdiv(batch, 32)), 4 waves = 4 blocks of 32 v rows
+// output side: grid (heads, vd / 32, cdiv(batch, 32)); the 4 waves of a
+// workgroup split the contraction (rank) in four and their 32x32 partial
+// products are summed through LDS
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(256) void mla_absorb_out_kernel(AbsorbOutArgs a) {
+  __shared__ f32x16 part[3][64];  // waves 1..3: one 32x32 fp32 block each
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = blockIdx.x;
-  const int b0 = blockIdx.y * kBTile;
+  const int vb = blockIdx.y;
+  const int b0 = blockIdx.z * kBTile;
   const int l32 = lane & 31, hi = lane >> 5;
   const bool brow_ok = b0 + l32 < a.batch;
-  // A: W_UV row v = 32*wave + lane%32 (k = rank index, 8 per lane-half);
+  const int kq = a.rank / 4;  // contraction quarter of this wave
+  // A: W_UV row v = 32*vb + lane%32 (k = rank index, 8 per lane-half);
   // B: o_lat^T column b0 + lane%32
-  const short* wrow = a.w + ((int64_t)h * (a.nope + a.vd) + a.nope + 32 * wave + l32) * a.w_s0 + 8 * hi;
-  const short* orow = a.o + (int64_t)(b0 + l32) * a.o_sb + (int64_t)h * a.o_sh + 8 * hi;
+  const short* wrow =
+      a.w + ((int64_t)h * (a.nope + a.vd) + a.nope + 32 * vb + l32) * a.w_s0 + wave * kq + 8 * hi;
+  const short* orow = a.o + (int64_t)(b0 + l32) * a.o_sb + (int64_t)h * a.o_sh + wave * kq + 8 * hi;
   f32x16 acc = (f32x16)0.0f;
-  constexpr int CH = 8;  // k steps per batch of loads
-  for (int k0 = 0; k0 < a.rank; k0 += 16 * CH) {
+  constexpr int CH = 8;  // k steps per batch of loads (all loads of a batch in flight together)
+  for (int k0 = 0; k0 < kq; k0 += 16 * CH) {
     i16x8 wa[CH], ob[CH];
 #pragma unroll
     for (int t = 0; t < CH; ++t) {
@@ -235,8 +235,12 @@ __global__ __launch_bounds__(256) void mla_absorb_out_kernel(AbsorbOutArgs a) {
 #pragma unroll
     for (int t = 0; t < CH; ++t) acc = Elt<DT>::mfma(wa[t], ob[t], acc);
   }
+  if (wave > 0) part[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  acc += part[0][lane] + part[1][lane] + part[2][lane];
   if (brow_ok) {
-    short* dst = a.out + (int64_t)(b0 + l32) * a.out_sb + (int64_t)h * a.vd + 32 * wave + 4 * hi;
+    short* dst = a.out + (int64_t)(b0 + l32) * a.out_sb + (int64_t)h * a.vd + 32 * vb + 4 * hi;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       i16x4 v;
@@ -318,7 +322,7 @@ int tmla_mla_absorb_q(const void* q_proj, int64_t q_proj_stride_b, const void* w
   if (batch < 0 || num_heads <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "batch must be >= 0 and num_heads > 0");
   if (dtype != TMLA_BF16 && dtype != TMLA_FP16) return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16 or TMLA_FP16");
   if (qk_nope_dim != kNope || qk_rope_dim != kRope || kv_lora_rank <= 0 || kv_lora_rank % kColsWG != 0 || v_head_dim <= 0)
-    return fail(TMLA_ERR_UNSUPPORTED, "absorb_q is built for qk_nope_dim 128, qk_rope_dim 64, kv_lora_rank a multiple of 256");
+    return fail(TMLA_ERR_UNSUPPORTED, "absorb_q is built for qk_nope_dim 128, qk_rope_dim 64, kv_lora_rank a multiple of 128");
   if (batch == 0) return TMLA_OK;
   if (!q_proj || !wkv_b || !positions || !q_out) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (((uintptr_t)q_proj | (uintptr_t)wkv_b | (uintptr_t)q_out) & 15)
@@ -355,8 +359,8 @@ int tmla_mla_absorb_out(const void* o_latent, int64_t o_stride_b, int64_t o_stri
                         void* stream) {
   if (batch < 0 || num_heads <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "batch must be >= 0 and num_heads > 0");
   if (dtype != TMLA_BF16 && dtype != TMLA_FP16) return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16 or TMLA_FP16");
-  if (v_head_dim != 128 || kv_lora_rank <= 0 || kv_lora_rank % 128 != 0 || qk_nope_dim < 0)
-    return fail(TMLA_ERR_UNSUPPORTED, "absorb_out is built for v_head_dim 128 and kv_lora_rank a multiple of 128");
+  if (v_head_dim <= 0 || v_head_dim % 32 != 0 || kv_lora_rank <= 0 || kv_lora_rank % 512 != 0 || qk_nope_dim < 0)
+    return fail(TMLA_ERR_UNSUPPORTED, "absorb_out is built for v_head_dim a multiple of 32 and kv_lora_rank a multiple of 512");
   if (batch == 0) return TMLA_OK;
   if (!o_latent || !wkv_b || !out) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (((uintptr_t)o_latent | (uintptr_t)wkv_b | (uintptr_t)out) & 15)
@@ -376,7 +380,7 @@ int tmla_mla_absorb_out(const void* o_latent, int64_t o_stride_b, int64_t o_stri
   a.nope = qk_nope_dim;
   a.rank = kv_lora_rank;
   a.vd = v_head_dim;
-  dim3 grid(num_heads, (batch + kBTile - 1) / kBTile);
+  dim3 grid(num_heads, v_head_dim / 32, (batch + kBTile - 1) / kBTile);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TMLA_BF16)
     hipLaunchKernelGGL(mla_absorb_out_kernel<TMLA_BF16>, grid, dim3(256), 0, s, a);
