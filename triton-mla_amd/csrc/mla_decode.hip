@@ -837,10 +837,17 @@ void mla_partial_kernel(PartialArgs a) {
           pv_iteration();
       }
     };
+    // Iteration -1 always runs with copies: for a segment of fewer than
+    // kStages - 1 sub-tiles its copy is of a clamped (valid) row into an
+    // entry no iteration reads, and the tail then never starts from the
+    // initial accumulators (which would have to be kept live across the
+    // first loop).
     int i = -1;
-    for (; i + kStages - 1 < nst; ++i) iteration(i, std::true_type{});
+    for (; i < 0 || i + kStages - 1 < nst; ++i) iteration(i, std::true_type{});
     for (; i < nst; ++i) iteration(i, std::false_type{});
-    // all waves must be done with the rings before they are reused below
+    // every copy has landed and all waves are done with the rings before the
+    // finalize reuses them
+    wait_vmcnt<0>();
     lds_barrier();
 
     // ---- finalize: out = acc / l, lse2 = m + log2(l) -------------------------
@@ -976,32 +983,38 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
     return;
   }
   static_assert(DV == 512, "one row = 64 lanes x 8 elements");
-  // Up to BATCH splits (the common case): every lse and partial row is
+  // Up to 16 splits (the common case): every lse and partial row is
   // requested at once, then m = max lse2 (-inf -> 0), w = 2^(lse2 - m).
   // Slots past `count` repeat the last written row with weight 0.
   constexpr int BATCH = 8;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   float wsum = 0.0f, m = -INFINITY;
-  if (count <= BATCH) {
-    float l[BATCH];
-    i16x8 v[BATCH];
+  auto merge_at_once = [&](auto NC) __attribute__((always_inline)) {
+    constexpr int N = decltype(NC)::value;
+    float l[N];
+    i16x8 v[N];
 #pragma unroll
-    for (int j = 0; j < BATCH; ++j) {
+    for (int j = 0; j < N; ++j) {
       const int64_t row = (int64_t)(slot0 + min(j, count - 1)) * a.num_heads + head;
       l[j] = a.mid_lse[row];
       v[j] = *reinterpret_cast<const i16x8*>(a.mid_o + row * DV + lane * 8);
     }
 #pragma unroll
-    for (int j = 0; j < BATCH; ++j)
+    for (int j = 0; j < N; ++j)
       if (j < count) m = fmaxf(m, l[j]);
     if (m == -INFINITY) m = 0.0f;
 #pragma unroll
-    for (int j = 0; j < BATCH; ++j) {
+    for (int j = 0; j < N; ++j) {
       const float w = j < count ? fast_exp2(l[j] - m) : 0.0f;
       wsum += w;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += w * Elt<DT>::to_float(v[j][e]);
     }
+  };
+  if (count <= BATCH) {
+    merge_at_once(std::integral_constant<int, BATCH>{});
+  } else if (count <= 2 * BATCH) {
+    merge_at_once(std::integral_constant<int, 2 * BATCH>{});
   } else {
     for (int s = lane; s < count; s += 64)
       m = fmaxf(m, a.mid_lse[(int64_t)(slot0 + s) * a.num_heads + head]);
