@@ -105,12 +105,12 @@ def main():
     for _ in range(args.warmup):
         if flush:
             flush()
-        call.partial()
-        call.combine()
+        call.run()
     torch.cuda.synchronize(dev)
 
-    # timed region: each step is partial + combine between two events on the
-    # launch stream (no event between the kernels, which would add a gap)
+    # timed region: each step is one mla_decode (tmla_mla_decode: partial +
+    # combine, no event between the kernels) between two events on the launch
+    # stream
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
     torch.cuda.synchronize(dev)
     wall0 = time.perf_counter()
@@ -118,8 +118,7 @@ def main():
         if flush:
             flush()
         ev[i][0].record(stream)
-        call.partial()
-        call.combine()
+        call.run()
         ev[i][1].record(stream)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - wall0
@@ -134,15 +133,28 @@ def main():
         evp[i][1].record(stream)
     torch.cuda.synchronize(dev)
 
+    # the single-launch form (tmla_mla_decode_fused, merge inside the partial
+    # kernel) on the same inputs, for comparison
+    ev1 = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        if flush:
+            flush()
+        ev1[i][0].record(stream)
+        call.run(single_launch=True)
+        ev1[i][1].record(stream)
+    torch.cuda.synchronize(dev)
+    single_out = call.out.clone()
+
     # the same step captured once in a HIP graph and replayed (how a serving
     # loop launches it): every replay must reproduce the eager result exactly
+    call.run()
+    torch.cuda.synchronize(dev)
     eager_out = call.out.clone()
     graph_ok = None
     try:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            call.partial()
-            call.combine()
+            call.run()
         graph_ok = True
         for _ in range(3):
             call.out.zero_()
@@ -165,6 +177,9 @@ def main():
 
     step_us = [e[0].elapsed_time(e[1]) * 1e3 for e in ev]
     partial_us = [e[0].elapsed_time(e[1]) * 1e3 for e in evp]
+    single_us = statistics.median([e[0].elapsed_time(e[1]) * 1e3 for e in ev1])
+    # the fused merge and stage 2 run the same merge code on the same partials
+    single_same = torch.equal(single_out, eager_out)
     us = statistics.median(step_us)
     p_us = statistics.fmean(partial_us)
 
@@ -198,6 +213,8 @@ def main():
                      "partial_us_mean": round(p_us, 2), "step_us_mean": round(statistics.fmean(step_us), 2),
                      "step_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "single_launch_us_per_step": round(single_us, 2) if call.fused else None,
+        "single_launch_matches": single_same,
         "wall_s_timed_region": round(wall, 4),
         "graph_replay_matches_eager": graph_ok,
     }

@@ -52,9 +52,12 @@ int tmla_version(void);
 
 /*
  * Bytes of device workspace tmla_mla_decode / _partial / _combine need:
- * partial outputs (input dtype [slots, H, head_dim_v]) and base-2 log-sum-exps
- * (float32 [slots, H]); slots = batch * num_splits (uniform) or
- * num_workers + batch (balanced).
+ * partial outputs (input dtype [slots, H, head_dim_v]), base-2 log-sum-exps
+ * (float32 [slots, H]) and the int32 counters of the fused merge;
+ * slots = batch * num_splits (uniform) or num_workers + batch (balanced).
+ * Zero-fill the workspace once before its first use by tmla_mla_decode;
+ * every call leaves the counters at zero again (a workspace may be reused
+ * by any later call with the same or smaller arguments, one call at a time).
  */
 size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v,
                             int32_t num_splits, int32_t num_workers);
@@ -104,8 +107,8 @@ int tmla_mla_decode_combine(const int32_t* seqlens, int32_t batch, int32_t num_h
                             size_t workspace_bytes, void* stream);
 
 /*
- * Both stages back to back: the whole of the reference's `mla_decode`
- * device work (src/triton_mla/kernel.py:264-320) for one call.
+ * Both stages back to back: the whole of the reference's `mla_decode` device
+ * work (src/triton_mla/kernel.py:264-320) for one call.
  */
 int tmla_mla_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
                     int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks,
@@ -116,8 +119,40 @@ int tmla_mla_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
                     int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/*
+ * The same call as ONE launch (no counterpart in the reference, which always
+ * launches two kernels): when every workgroup of stage 1 fits on the device
+ * at once (workers times head blocks of up to 128 heads at most the CU
+ * count), the workers of a split sequence merge its partials themselves,
+ * each a share of the heads, once all of them have stored theirs (a bounded
+ * wait: a worker that stops waiting hands its share to the one whose arrival
+ * completes the count). Otherwise it runs both stages like tmla_mla_decode.
+ * Results equal tmla_mla_decode's bit for bit. The workspace must be
+ * zero-filled before its first use (tmla_workspace_bytes). On MI355X the
+ * two-kernel form is as fast or faster for the measured shapes (the merge
+ * reads back every partial either way); this form is for callers that need
+ * a single launch.
+ */
+int tmla_mla_decode_fused(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                          int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks,
+                          int32_t page_size, const int32_t* block_table, int64_t bt_stride_b,
+                          int32_t bt_cols, const int32_t* seqlens, int32_t batch, int32_t num_heads,
+                          int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale,
+                          int32_t num_splits, int32_t num_workers, void* out, int64_t out_stride_b,
+                          int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 /* Number of compute units of `device` (0 on error); the default worker count. */
 int32_t tmla_device_cu_count(int32_t device);
+
+/*
+ * Test hook, no counterpart in the reference: the number of polls (about
+ * 2^7 clocks apart) a worker of the fused merge waits for its siblings
+ * before it hands its share over; polls < 0 only queries. Returns the
+ * previous value (default 16384). 0 makes every share go to the worker that
+ * completes the count, which tests that path.
+ */
+int32_t tmla_set_merge_spin_limit(int32_t polls);
 
 /*
  * MLA layer glue: the absorbed-projection steps on either side of

@@ -41,14 +41,19 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_workspace_arithmetic(lib):
-    # uniform: batch * splits slots; balanced: workers + batch slots (16-bit partial + float32 lse)
-    def expect(slots, heads, dv=512):
-        o = slots * heads * dv * 2
-        return ((o + 255) // 256) * 256 + slots * heads * 4
+    # uniform: batch * splits slots; balanced: workers + batch slots (16-bit
+    # partial + float32 lse, each region 256-byte aligned), then the fused
+    # merge's int32 counters: 2 per (sequence, head block) and 1 per
+    # (slot, head block), head blocks of up to 128 heads
+    def expect(batch, slots, heads, dv=512):
+        al = lambda x: (x + 255) // 256 * 256
+        gy = -(-heads // (32 if heads <= 32 else 64 if heads <= 64 else 128))
+        return al(slots * heads * dv * 2) + al(slots * heads * 4) + (2 * batch + slots) * gy * 4
 
-    assert lib.tmla_workspace_bytes(32, 128, 512, 8, 0) == expect(256, 128)
-    assert lib.tmla_workspace_bytes(32, 128, 512, 0, 256) == expect(288, 128)
-    assert lib.tmla_workspace_bytes(3, 20, 512, 1, 0) == expect(3, 20)
+    assert lib.tmla_workspace_bytes(32, 128, 512, 8, 0) == expect(32, 256, 128)
+    assert lib.tmla_workspace_bytes(32, 128, 512, 0, 256) == expect(32, 288, 128)
+    assert lib.tmla_workspace_bytes(3, 20, 512, 1, 0) == expect(3, 3, 20)
+    assert lib.tmla_workspace_bytes(4, 256, 512, 2, 0) == expect(4, 8, 256)
     assert lib.tmla_version() >= 100
 
 

@@ -1,0 +1,159 @@
+"""The single-launch decode (tmla_mla_decode_fused: the log-sum-exp merge of
+the split partials done inside the partial kernel) against the two-kernel
+form (tmla_mla_decode_partial + tmla_mla_decode_combine, the reference's two
+launches, src/triton_mla/kernel.py:276-320) on the same inputs.
+
+Both forms merge the same stored partials with the same code in the same
+order, so out and lse must agree bit for bit; the two-kernel form itself is
+checked against the oracle in test_kernel_gpu.py and test_configs_gpu.py, and
+here the headline case is also checked against the oracle directly.
+
+Covered: balanced partitions with 1, 8, 16 and more than 16 workers per
+sequence; workers whose range straddles two split sequences (both of their
+merge records in use); the uniform split; empty sequences (out = 0,
+lse = -inf, cleared by the single launch itself); 16, 64, 128 and 200 heads
+(one or two head blocks per worker); fp16; repeated calls on one workspace
+(the merge counters return to zero); the hand-over path (spin limit 0: every
+worker that does not complete the count gives its share to the one that
+does); and HIP-graph replays.
+"""
+
+import pytest
+import torch
+
+import oracle
+from conftest import bits, dtype_name
+
+pytestmark = pytest.mark.gpu
+
+
+def launch(inp, gpu, num_splits=None, num_workers=None):
+    from triton_mla.kernel import DecodeLaunch
+
+    d = inp.to(gpu)
+    return DecodeLaunch(d.q, d.kv_cache, d.seqlens, d.block_table, 512, d.softmax_scale, num_splits, num_workers)
+
+
+def two_stage(call):
+    call.out.fill_(1.0)
+    call.lse.fill_(1.0)
+    call.partial()
+    call.combine()
+    torch.cuda.synchronize()
+    return call.out.clone(), call.lse.clone()
+
+
+def single(call):
+    call.out.fill_(1.0)  # every element must be written by the launch
+    call.lse.fill_(1.0)
+    call.run(single_launch=True)
+    torch.cuda.synchronize()
+    return call.out.clone(), call.lse.clone()
+
+
+def assert_same(a, b, what):
+    (oa, la), (ob, lb) = a, b
+    assert torch.equal(oa.view(torch.int16), ob.view(torch.int16)), f"{what}: out differs"
+    assert torch.equal(la.view(torch.int32), lb.view(torch.int32)), f"{what}: lse differs"
+
+
+def case(name):
+    from triton_mla import workloads
+
+    if name == "b32_h128_8k":
+        return workloads.b32_h128_8k()
+    if name == "b1_h128_1k":
+        return workloads.b1_h128_1k()
+    if name == "ragged_h128":  # empty, 1-token and long sequences
+        inp = workloads.ragged(12, 128, 0, 6000, seed=5)
+        inp.seqlens[[2, 7]] = torch.tensor([0, 1], dtype=torch.int32)
+        return inp
+    if name == "ragged_h16":
+        return workloads.ragged(40, 16, 0, 3000, seed=6)
+    if name == "ragged_h64_fp16":
+        return workloads.ragged(9, 64, 1, 5000, dtype=torch.float16, seed=7)
+    if name == "ragged_h200":
+        return workloads.ragged(6, 200, 0, 4000, seed=8)
+    raise KeyError(name)
+
+
+# (case, num_splits, num_workers): workers per split sequence from 1 to > 16;
+# 7 and 24 workers give ranges that straddle sequence ends
+CASES = [
+    ("b32_h128_8k", None, None),      # 8 workers per sequence
+    ("b1_h128_1k", None, None),       # 16 workers per sequence
+    ("ragged_h128", None, None),      # up to ~90 workers per sequence, one-tile chunks
+    ("ragged_h128", None, 7),         # straddling ranges
+    ("ragged_h128", 4, None),         # uniform split
+    ("ragged_h16", None, 24),
+    ("ragged_h64_fp16", None, None),
+    ("ragged_h64_fp16", 3, None),
+    ("ragged_h200", None, 100),       # two head blocks per worker
+]
+
+
+@pytest.mark.parametrize("name,splits,workers", CASES)
+def test_single_launch_equals_two_kernels(gpu, name, splits, workers):
+    inp = case(name)
+    call = launch(inp, gpu, splits, workers)
+    assert call.fused, "the case must take the single-launch path"
+    ref = two_stage(call)
+    for rep in range(3):  # the same workspace again: the counters were reset
+        assert_same(single(call), ref, f"{name} splits={splits} workers={workers} call {rep}")
+    call.run()  # tmla_mla_decode: the two kernels
+    torch.cuda.synchronize()
+    assert_same((call.out.clone(), call.lse.clone()), ref, f"{name} tmla_mla_decode")
+    empty = inp.seqlens == 0
+    if bool(empty.any()):
+        out, lse = single(call)
+        assert torch.all(out[empty.to(gpu)] == 0) and torch.all(torch.isneginf(lse[empty.to(gpu)]))
+
+
+@pytest.mark.parametrize("name,splits,workers", [CASES[0], CASES[2], CASES[3], CASES[5]])
+def test_hand_over_path(gpu, name, splits, workers):
+    """Spin limit 0: a worker that does not complete its sequence's count
+    hands its share over at once; the worker that completes the count merges
+    it. Same bits as the two-kernel form, and the counters still reset."""
+    from triton_mla import _native
+
+    lib = _native.load()
+    call = launch(case(name), gpu, splits, workers)
+    ref = two_stage(call)
+    prev = lib.tmla_set_merge_spin_limit(0)
+    try:
+        assert_same(single(call), ref, f"{name} hand-over")
+        assert_same(single(call), ref, f"{name} hand-over, second call")
+    finally:
+        lib.tmla_set_merge_spin_limit(prev)
+    assert_same(single(call), ref, f"{name} after hand-over")
+
+
+def test_headline_against_oracle(gpu):
+    """B=32, H=128, 8K context through the single launch, checked against the
+    float64 oracle on the first two sequences (atol = rtol = 1e-2)."""
+    inp = case("b32_h128_8k")
+    call = launch(inp, gpu)
+    out, lse = single(call)
+    n = 2
+    ref_out, ref_lse = oracle.mla_decode_ref(bits(inp.q[:n]), bits(inp.kv_cache), inp.seqlens[:n].numpy(),
+                                             inp.block_table[:n].numpy(), 512, inp.softmax_scale,
+                                             dtype=dtype_name(inp.q.dtype))
+    torch.testing.assert_close(out[:n].float().cpu(), torch.from_numpy(ref_out), atol=1e-2, rtol=1e-2)
+    torch.testing.assert_close(lse[:n].cpu(), torch.from_numpy(ref_lse), atol=1e-3, rtol=1e-3)
+
+
+def test_graph_replays(gpu):
+    """The single launch captured in a HIP graph: every replay (with eager
+    work and synchronisation in between) reproduces the eager result."""
+    call = launch(case("ragged_h128"), gpu)
+    eager = single(call)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call.run(single_launch=True)
+    for rep in range(4):
+        call.out.fill_(1.0)
+        call.lse.fill_(1.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_same((call.out.clone(), call.lse.clone()), eager, f"graph replay {rep}")
+        torch.randn(1024, device=gpu).sum().item()  # eager work between replays

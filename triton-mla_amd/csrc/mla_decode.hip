@@ -68,6 +68,14 @@ struct PartialArgs {
   float* lse;
   short* mid_o;            // [slots, H, DV] normalised partials, input dtype
   float* mid_lse;          // [slots, H], base-2
+  // In-kernel merge (fused): the workers of a split sequence each merge one
+  // share of its heads once all of them have stored their partials.
+  int32_t fused;
+  int32_t spin_limit;      // polls before a waiting worker hands its share over
+  int32_t* m_count;        // [batch, head blocks] partials stored
+  int32_t* m_done;         // [batch, head blocks] shares merged
+  int32_t* m_flag;         // [slots, head blocks] 0 owner merges, 1 handed over, 2 taken over
+  int32_t mid_o_bytes;     // bytes of the partial rows (< 2^31 when fused)
 };
 
 struct CombineArgs {
@@ -109,6 +117,14 @@ __device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x))
 // (Operand-constrained asm lives in __device__ helpers only: the host pass
 // of the compiler rejects GPU register constraints inside a kernel body.)
 __device__ __forceinline__ void pin_f1(float& a) { asm volatile("" : "+v"(a)); }
+__device__ __forceinline__ void pin_i1(int& a) { asm volatile("" : "+v"(a)); }
+// A uniform value the compiler must treat as new at this point: divisions by
+// it are not hoisted out of the enclosing loop (their reciprocal would occupy
+// a VGPR for the whole loop).
+__device__ __forceinline__ int fresh_s(int x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
 __device__ __forceinline__ void pin_f2(float& a, float& b) { asm volatile("" : "+v"(a), "+v"(b)); }
 __device__ __forceinline__ void pin_f3(float& a, float& b, float& c) { asm volatile("" : "+v"(a), "+v"(b), "+v"(c)); }
 __device__ __forceinline__ void pin_f4(f32x4& x) { asm volatile("" : "+v"(x)); }
@@ -159,14 +175,20 @@ __device__ __forceinline__ void lgkm_tie(i16x8& k, i16x4& vl, i16x4& vh, i16x8& 
     asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(p) : "i"(N));
 }
 
-// LDS reads issued by fetch(t) of a pass (one K operand per S step; from step
-// PVOFF on, two V^T halves at the first head block of a PV column block and
+// Step t of a pass carries PV step PV0 + (t - PVOFF) / PVS when t >= PVOFF
+// and (t - PVOFF) is a multiple of PVS below NV * PVS.
+constexpr bool pass_has_pv(int t, int NV, int PVOFF, int PVS) {
+  return t >= PVOFF && (t - PVOFF) % PVS == 0 && (t - PVOFF) / PVS < NV;
+}
+
+// LDS reads issued by fetch(t) of a pass (one K operand per S step; on the
+// PV steps, two V^T halves at the first head block of a PV column block and
 // one P^T operand at the first column block of a (token half, head block)).
-template <int NS, int NV, int PV0, int NHB, int PVOFF>
+template <int NS, int NV, int PV0, int NHB, int PVOFF, int PVS>
 constexpr int pass_reads(int t) {
   int n = t < NS ? 1 : 0;
-  if (t >= PVOFF && t - PVOFF < NV) {
-    const int g = PV0 + t - PVOFF;
+  if (pass_has_pv(t, NV, PVOFF, PVS)) {
+    const int g = PV0 + (t - PVOFF) / PVS;
     n += (g % NHB == 0 ? 2 : 0) + ((g % (4 * NHB)) / NHB == 0 ? 1 : 0);
   }
   return n;
@@ -218,6 +240,305 @@ __device__ __forceinline__ void mfma_vgpr_fence(f32x16& d) {
 // generates, but cannot see into this asm.
 __device__ __forceinline__ void store_through(i16x8* p, i16x8 v) {
   asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_through_f32(float* p, float v) {
+  asm volatile("global_store_dword %0, %1, off sc0 sc1" : : "v"(p), "v"(v) : "memory");
+}
+
+// ---------------------------------------------------------------------------
+// Log-sum-exp merge of split partials (kernel.py:159-181), shared by the
+// combine kernel and the fused merge of the partial kernel:
+//   m = max_j lse2_j (-inf -> 0), w_j = 2^(lse2_j - m),
+//   out = sum_j w_j o_j / sum_j w_j, lse = (m + log2 sum_j w_j) ln 2.
+// One wave per head row (64 lanes x 8 elements of 512).
+// ---------------------------------------------------------------------------
+struct MergeView {
+  const short* mid_o;    // [slots, H, 512]
+  const float* mid_lse;  // [slots, H]
+  int32_t num_heads;
+  char* out;
+  int64_t out_sb, out_sh;
+  float* lse;            // [batch, H], natural log
+};
+
+// Partial rows and lse values written by an earlier launch (stage 2).
+struct PlainLoads {
+  const short* mid_o;
+  const float* mid_lse;
+  __device__ __forceinline__ float lse(int64_t row) const { return mid_lse[row]; }
+  __device__ __forceinline__ i16x8 rowv(int64_t row, int lane) const {
+    return *reinterpret_cast<const i16x8*>(mid_o + row * 512 + lane * 8);
+  }
+};
+
+// Written by other workgroups of the same launch (the fused merge): loads
+// that bypass this CU's L1 and the L2 (system-coherent, sc0 sc1) see the
+// write-through stores of the partials without any cache maintenance. Byte
+// offsets are 32-bit (the host keeps the partials below 2 GiB).
+// Buffer resource word 3 of gfx9-family raw buffers (32-bit data format).
+constexpr int kBufferWord3 = 0x00020000;
+
+struct CoherentLoads {
+  __amdgpu_buffer_rsrc_t ro, rl;
+  static constexpr int kSysCoherent = 1 | 16;  // sc0 | sc1
+  __device__ __forceinline__ float lse(int64_t row) const {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, (int)row * 4, 0, kSysCoherent));
+  }
+  __device__ __forceinline__ i16x8 rowv(int64_t row, int lane) const {
+    return __builtin_bit_cast(i16x8, __builtin_amdgcn_raw_buffer_load_b128(ro, (int)row * 1024 + lane * 16, 0,
+                                                                           kSysCoherent));
+  }
+};
+
+template <int DT>
+__device__ __forceinline__ void merge_store(const MergeView& mv, int b, int head, const float (&acc)[8], float wsum,
+                                            float m, int lane) {
+  const float inv = wsum > 0.0f ? 1.0f / wsum : 1.0f;
+  i16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = Elt<DT>::from_float(acc[e] * inv);
+  short* orow = reinterpret_cast<short*>(mv.out) + (int64_t)b * mv.out_sb + (int64_t)head * mv.out_sh;
+  *reinterpret_cast<i16x8*>(orow + lane * 8) = o;
+  if (lane == 0) mv.lse[(int64_t)b * mv.num_heads + head] = wsum > 0.0f ? (m + fast_log2(wsum)) * kLn2 : -INFINITY;
+}
+
+// Empty sequence: out = 0, lse = -inf (kernel.py:126-128, 178-181).
+__device__ __forceinline__ void merge_zero(const MergeView& mv, int b, int head, int lane) {
+  short* orow = reinterpret_cast<short*>(mv.out) + (int64_t)b * mv.out_sb + (int64_t)head * mv.out_sh;
+  *reinterpret_cast<i16x8*>(orow + lane * 8) = (i16x8)0;
+  if (lane == 0) mv.lse[(int64_t)b * mv.num_heads + head] = -INFINITY;
+}
+
+// Heads [head, head + nh), nh <= NH, over slots [slot0, slot0 + count),
+// count <= NR: every lse and row load is issued before the first use. Slots
+// past `count` repeat the last one with weight 0; heads past `nh` repeat the
+// last head and are not stored.
+template <int DT, int NH, int NR, class LD>
+__device__ __forceinline__ void merge_rows_at_once(const MergeView& mv, const LD& ld, int b, int head, int nh,
+                                                   int slot0, int count, int lane) {
+  float l[NH][NR];
+  i16x8 v[NH][NR];
+  // row indices in VGPRs: vector address arithmetic instead of one scalar
+  // register pair per row
+  int r0 = slot0 * mv.num_heads + head;
+  pin_i1(r0);
+#pragma unroll
+  for (int i = 0; i < NH; ++i) {
+    const int hh = min(i, nh - 1);
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      const int64_t row = (int64_t)(r0 + min(j, count - 1) * mv.num_heads + hh);
+      l[i][j] = ld.lse(row);
+      v[i][j] = ld.rowv(row, lane);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NH; ++i) {
+    if (i >= nh) break;
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NR; ++j)
+      if (j < count) m = fmaxf(m, l[i][j]);
+    if (m == -INFINITY) m = 0.0f;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, wsum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      const float w = j < count ? fast_exp2(l[i][j] - m) : 0.0f;
+      wsum += w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += w * Elt<DT>::to_float(v[i][j][e]);
+    }
+    merge_store<DT>(mv, b, head + i, acc, wsum, m, lane);
+  }
+}
+
+// Any count: the max over all slots first, then eight rows in flight per batch.
+template <int DT, class LD>
+__device__ __forceinline__ void merge_row_loop(const MergeView& mv, const LD& ld, int b, int head, int slot0,
+                                               int count, int lane) {
+  constexpr int BATCH = 8;
+  float m = -INFINITY;
+  for (int s = lane; s < count; s += 64) m = fmaxf(m, ld.lse((int64_t)(slot0 + s) * mv.num_heads + head));
+  for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+  if (m == -INFINITY) m = 0.0f;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, wsum = 0.0f;
+  for (int s0 = 0; s0 < count; s0 += BATCH) {
+    float w[BATCH];
+    i16x8 v[BATCH];
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      const int sj = s0 + j;
+      const int64_t row = (int64_t)(slot0 + min(sj, count - 1)) * mv.num_heads + head;
+      w[j] = sj < count ? fast_exp2(ld.lse(row) - m) : 0.0f;
+      v[j] = ld.rowv(row, lane);
+    }
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      wsum += w[j];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += w[j] * Elt<DT>::to_float(v[j][e]);
+    }
+  }
+  merge_store<DT>(mv, b, head, acc, wsum, m, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Fused merge (single launch): run by every workgroup of the partial kernel
+// after its last segment.
+//
+// The c workers of a split sequence b (per head block of a workgroup) each
+// store their partial, then add 1 to m_count[b]. Sibling k then merges share
+// k of the workgroup's heads, heads [k*nh/c, (k+1)*nh/c), once m_count[b]
+// reaches c. The wait is bounded (spin_limit polls): a worker that runs out
+// hands its share over (m_flag 0 -> 1) and then reads m_count again with a
+// read-modify-write; if all have arrived by then it takes the share back
+// (1 -> 2) and merges it itself, else the worker whose arrival completed the
+// count finds the flag at 1 and takes the share over (1 -> 2). Every share is
+// merged exactly once and no worker waits without bound, whether or not the
+// siblings are resident together. The worker that completes m_done[b]
+// (shares merged) resets the sequence's counters and flags to zero, so the
+// workspace is ready for the next launch.
+//
+// Coherence without cache maintenance: partial rows and lse values are
+// stored write-through at system scope (sc0 sc1) and their stores have
+// completed (vmcnt 0) before the arrival; counters and flags are system-scope
+// atomics, performed at memory; merges read the partials with loads that
+// bypass L1 and L2 (CoherentLoads). A release/acquire at agent scope would
+// instead write back and invalidate the whole L2 of the XCD for every
+// arrival and merge. Two atomics whose order matters are separated by a wait
+// for the first one's completion.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void mem_wait_all() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ int sys_load(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ int sys_add(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ bool sys_cas(int* p, int expect, int desired) {
+  return __hip_atomic_compare_exchange_strong(p, &expect, desired, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void sys_store(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+template <int DT>
+__device__ __forceinline__ void merge_share(const MergeView& mv, const CoherentLoads& ld, int b, int j, int c, int s0,
+                                            int hb0, int nh, int wave, int lane) {
+  const int h_lo = hb0 + (j * nh) / c, h_hi = hb0 + ((j + 1) * nh) / c;
+  if (c <= 8) {
+    for (int h = h_lo + 4 * wave; h < h_hi; h += 16)
+      merge_rows_at_once<DT, 4, 8>(mv, ld, b, h, min(4, h_hi - h), s0, c, lane);
+  } else if (c <= 16) {
+    for (int h = h_lo + 2 * wave; h < h_hi; h += 8)
+      merge_rows_at_once<DT, 2, 16>(mv, ld, b, h, min(2, h_hi - h), s0, c, lane);
+  } else {
+    for (int h = h_lo + wave; h < h_hi; h += 4) merge_row_loop<DT>(mv, ld, b, h, s0, c, lane);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void fused_merge_tail(const MergeView& mv, const CoherentLoads& ld, int32_t* m_count,
+                                                 int32_t* m_done, int32_t* m_flag, int spin_limit, int wave,
+                                                 int (*s_pend)[5], int* s_msg, int nhb) {
+  const int lane = lane_id_fresh();
+  const int gy = gridDim.y, y = blockIdx.y;
+  const int hb0 = y * (kHeadsPerWave * nhb);
+  const int nh = min(kHeadsPerWave * nhb, mv.num_heads - hb0);
+  mem_wait_all();
+  lds_barrier();  // the merge records written by thread 0
+  for (int p = 0; p < 2; ++p) {
+    const int b = s_pend[p][0], k = s_pend[p][1], c = s_pend[p][2], s0 = s_pend[p][3];
+    if (b < 0) continue;
+    int* cnt = m_count + (int64_t)b * gy + y;
+    int* done = m_done + (int64_t)b * gy + y;
+    int* flag = m_flag + (int64_t)s0 * gy + y;  // sibling j: flag[j * gy]
+    if (wave == 0) {
+      const bool last = s_pend[p][4] != 0;
+      int own = last ? 1 : 0;
+      if (!last) {
+        int v = 0;
+        for (int it = 0;; ++it) {
+          int x = 0;
+          if (lane == 0) x = sys_load(cnt);
+          v = __builtin_amdgcn_readfirstlane(x);
+          if (v >= c || it >= spin_limit) break;
+          __builtin_amdgcn_s_sleep(2);
+        }
+        if (v >= c) {
+          own = 1;
+        } else {
+          int r = 0;
+          if (lane == 0) {
+            int* fk = flag + (int64_t)k * gy;
+            sys_cas(fk, 0, 1);
+            mem_wait_all();  // the hand-over is in place before the count is read again
+            const int v2 = sys_add(cnt, 0);
+            mem_wait_all();
+            if (v2 >= c) r = sys_cas(fk, 1, 2) ? 1 : 0;
+          }
+          own = __builtin_amdgcn_readfirstlane(r);
+        }
+      }
+      if (lane == 0) {
+        s_msg[0] = own;
+        s_msg[1] = last ? 1 : 0;
+      }
+    }
+    mem_wait_all();
+    lds_barrier();
+    const int own = s_msg[0], last = s_msg[1];
+    int merged = 0;
+    if (own) {
+      merge_share<DT>(mv, ld, b, k, c, s0, hb0, nh, wave, lane);
+      merged = 1;
+    }
+    if (last) {
+      // shares handed over by siblings that stopped waiting
+      for (int j0 = 0; j0 < c; j0 += 64) {
+        mem_wait_all();
+        lds_barrier();  // every wave has read s_msg
+        if (wave == 0) {
+          const int j = j0 + lane;
+          bool won = false;
+          if (j < c && j != k) {
+            int* fj = flag + (int64_t)j * gy;
+            if (sys_load(fj) == 1) won = sys_cas(fj, 1, 2);
+          }
+          const uint64_t mask = __ballot(won);
+          if (lane == 0) {
+            s_msg[2] = (int)(uint32_t)mask;
+            s_msg[3] = (int)(uint32_t)(mask >> 32);
+          }
+        }
+        mem_wait_all();
+        lds_barrier();
+        uint64_t mask = (uint64_t)(uint32_t)s_msg[2] | ((uint64_t)(uint32_t)s_msg[3] << 32);
+        while (mask != 0) {
+          const int j = j0 + __builtin_ctzll(mask);
+          mask &= mask - 1;
+          merge_share<DT>(mv, ld, b, j, c, s0, hb0, nh, wave, lane);
+          ++merged;
+        }
+      }
+    }
+    // the worker whose shares complete the count resets b's state
+    if (wave == 0 && merged > 0) {
+      int r = 0;
+      if (lane == 0) r = sys_add(done, merged) + merged == c;
+      if (__builtin_amdgcn_readfirstlane(r)) {
+        for (int j = lane; j < c; j += 64) sys_store(flag + (int64_t)j * gy, 0);
+        if (lane == 0) {
+          sys_store(cnt, 0);
+          sys_store(done, 0);
+        }
+      }
+    }
+    mem_wait_all();
+    lds_barrier();  // s_msg is rewritten for the next record
+  }
 }
 
 // Byte offset of the row of (local) token `tok` of sequence b inside kv.
@@ -308,6 +629,11 @@ void mla_partial_kernel(PartialArgs a) {
 
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
   char LDS_AS* const lds = (char LDS_AS*)(void LDS_AS*)smem;
+  // fused merge: the split segments awaiting their merge ({b, index among
+  // b's workers, their count, b's first slot, arrived last}) and the merge
+  // decisions wave 0 hands to the other waves
+  __shared__ int s_pend[2][5];
+  __shared__ int s_msg[4];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar LDS bases
@@ -321,6 +647,12 @@ void mla_partial_kernel(PartialArgs a) {
                          : (int)blockIdx.x;
   const bool s_owner = NHB == 4 || wave < NHB;  // runs S and the softmax of head block `wave`
   const int head_base = blockIdx.y * (kHeadsPerWave * NHB) + wave * kHeadsPerWave;
+  // fused merge: this worker clears sequences worker, worker + nwg, ... when
+  // they are empty; the first length is requested now, used at the end
+  const int pre_len = __builtin_amdgcn_readfirstlane((a.fused && worker < a.batch) ? a.seqlens[worker] : 1);
+  // split segments awaiting their merge: at most the first (record 0) and
+  // the last (record 1) segment of the worker's range; b < 0 = none
+  if (a.fused && tid == 0) s_pend[0][0] = s_pend[1][0] = -1;
 
   // ---- work range -------------------------------------------------------
   int b_first, tile_lo, tile_hi, off_first, n_first, chunk = 0;
@@ -356,23 +688,40 @@ void mla_partial_kernel(PartialArgs a) {
     const int total = __builtin_amdgcn_readlane(incl, 63);
     chunk = (total + a.num_workers - 1) / a.num_workers;
     const int lo = worker * chunk;
-    if (lo >= total) return;  // wave-uniform, and the same in every wave
-    // the one lane whose sequences hold tile lo finds which of them it is
-    int off = incl - sum, fb = lo_b, flen = len0;
-    for (int b = lo_b; b < hi_b; ++b) {
-      const int len = b == lo_b ? len0 : a.seqlens[b];
-      const int nt = tiles_of(len);
-      fb = b;
-      flen = len;
-      if (lo < off + nt) break;
-      off += nt;
+    if (lo >= total) {  // wave-uniform, and the same in every wave
+      if (!a.fused) return;  // (the fused tail still clears empty sequences)
+      b_first = off_first = n_first = tile_lo = tile_hi = 0;
+    } else {
+      // the one lane whose sequences hold tile lo finds which of them it is
+      int off = incl - sum, fb = lo_b, flen = len0;
+      for (int b = lo_b; b < hi_b; ++b) {
+        const int len = b == lo_b ? len0 : a.seqlens[b];
+        const int nt = tiles_of(len);
+        fb = b;
+        flen = len;
+        if (lo < off + nt) break;
+        off += nt;
+      }
+      const int src = __builtin_ctzll(__ballot(sum > 0 && incl - sum <= lo && lo < incl));
+      b_first = __builtin_amdgcn_readlane(fb, src);
+      off_first = __builtin_amdgcn_readlane(off, src);
+      n_first = __builtin_amdgcn_readlane(flen, src);
+      tile_lo = lo - off_first;                      // local to b_first
+      tile_hi = min(lo + chunk, total) - off_first;  // may run past b_first
     }
-    const int src = __builtin_ctzll(__ballot(sum > 0 && incl - sum <= lo && lo < incl));
-    b_first = __builtin_amdgcn_readlane(fb, src);
-    off_first = __builtin_amdgcn_readlane(off, src);
-    n_first = __builtin_amdgcn_readlane(flen, src);
-    tile_lo = lo - off_first;                      // local to b_first
-    tile_hi = min(lo + chunk, total) - off_first;  // may run past b_first
+  }
+  if (a.fused) {
+    // empty sequences worker, worker + nwg, ...: out = 0, lse = -inf
+    // (kernel.py:126-128, 178-181); the first length was requested at entry
+    const int lane = lane_id_fresh();
+    const int hb0 = blockIdx.y * (kHeadsPerWave * NHB);
+    const int nh = min(kHeadsPerWave * NHB, a.num_heads - hb0);
+    const MergeView mv{a.mid_o, a.mid_lse, a.num_heads, a.out, a.out_sb, a.out_sh, a.lse};
+    for (int bb = worker; bb < a.batch; bb += nwg) {
+      const int len = bb == worker ? pre_len : a.seqlens[bb];
+      if (tiles_of(len) == 0)
+        for (int h = hb0 + wave; h < hb0 + nh; h += 4) merge_zero(mv, bb, h, lane);
+    }
   }
   if (tile_lo >= tile_hi) return;
 
@@ -439,10 +788,27 @@ void mla_partial_kernel(PartialArgs a) {
       const int count = (nt_b + spt - 1) / spt;
       seg.slot = b * S + t_start / spt;
       seg.direct = count == 1;
+      // fused merge record: b, this worker's index among b's workers, their
+      // count, b's first slot
+      if (a.fused && !seg.direct && wave == 0 && lane == 0) {
+        int* r = s_pend[b == b_first ? 0 : 1];
+        r[0] = b;
+        r[1] = t_start / spt;
+        r[2] = count;
+        r[3] = b * S;
+      }
     } else {
-      const int g1 = seg_global_off / chunk, g2 = (seg_global_off + nt_b - 1) / chunk;
+      const int ch = fresh_s(chunk);
+      const int g1 = seg_global_off / ch, g2 = (seg_global_off + nt_b - 1) / ch;
       seg.slot = worker + b;
       seg.direct = g1 == g2;
+      if (a.fused && !seg.direct && wave == 0 && lane == 0) {
+        int* r = s_pend[b == b_first ? 0 : 1];
+        r[0] = b;
+        r[1] = worker - g1;
+        r[2] = g2 - g1 + 1;
+        r[3] = g1 + b;
+      }
     }
 
     // O^T of this wave's dims: block j4 * NHB + hb = dims 32 * j4 (of the
@@ -541,15 +907,21 @@ void mla_partial_kernel(PartialArgs a) {
     constexpr int PV_SPLIT = SPC;      // token half 0 beside S, half 1 beside the softmax
     constexpr int PV_START = 4;        // S-only steps first: the rescale factors arrive meanwhile
     constexpr int SM_STEPS = 11;       // steps the softmax pieces need in pass 2
+    // pass 1 of an S wave: one PV step every PV_STRIDE S steps, so that the
+    // time between a read and its use (PD steps) never shrinks to PD bare S
+    // steps
+    constexpr int PV_STRIDE = 2;
     static_assert(NDBW == 4, "four 32-dim blocks per wave");
-    auto pass = [&](auto DOS, auto PVLO, auto PVHI, auto PVOFFC, auto MINSTEPS, const char LDS_AS* kst_v,
+    auto pass = [&](auto DOS, auto PVLO, auto PVHI, auto PVOFFC, auto PVSC, auto MINSTEPS, const char LDS_AS* kst_v,
                     const char LDS_AS* kst_r, const char LDS_AS* vst, const char LDS_AS* pst, f32x16& s, auto&& hook)
                     __attribute__((always_inline)) {
       constexpr bool do_s = decltype(DOS)::value;
       constexpr int PV0 = decltype(PVLO)::value;
       constexpr int PVOFF = decltype(PVOFFC)::value;
+      constexpr int PVS = decltype(PVSC)::value;
       constexpr int NS = do_s ? NKC : 0, NV = decltype(PVHI)::value - PV0;
-      constexpr int NSTEPS0 = NS > NV + PVOFF ? NS : NV + PVOFF;
+      constexpr int PV_END = PVOFF + (NV - 1) * PVS + 1;  // one past the last PV step
+      constexpr int NSTEPS0 = NS > PV_END ? NS : PV_END;
       constexpr int NSTEPS = NSTEPS0 > decltype(MINSTEPS)::value ? NSTEPS0 : decltype(MINSTEPS)::value;
       const char LDS_AS* kvb[4] = {kst_v + k_off_v[0], kst_v + k_off_v[1], kst_v + k_off_v[2], kst_v + k_off_v[3]};
       const char LDS_AS* krb[4] = {kst_r + k_off_r[0], kst_r + k_off_r[1], kst_r + k_off_r[2], kst_r + k_off_r[3]};
@@ -567,8 +939,8 @@ void mla_partial_kernel(PartialArgs a) {
           else
             kb[t % (PD + 1)] = ds_read_b128<(cb - NVB) * 1024>(krb[t & 3]);
         }
-        if constexpr (t >= PVOFF && t - PVOFF < NV) {
-          constexpr int g = PV0 + t - PVOFF, c = g / SPC, j4 = (g % SPC) / NHB, hb = g % NHB;
+        if constexpr (pass_has_pv(t, NV, PVOFF, PVS)) {
+          constexpr int g = PV0 + (t - PVOFF) / PVS, c = g / SPC, j4 = (g % SPC) / NHB, hb = g % NHB;
           if constexpr (hb == 0) {
             constexpr int off = c * 2 * NVB * 1024 + (j4 >> 1) * 1024;
             vl[c * NDBW + j4] = ds_read_tr<off>(vbase[j4 & 1][0]);
@@ -585,11 +957,11 @@ void mla_partial_kernel(PartialArgs a) {
         constexpr int last = (j + PD < NSTEPS - 1) ? j + PD : NSTEPS - 1;
         constexpr int after = [] {
           int n = 0;
-          for (int t = j + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NHB, PVOFF>(t);
+          for (int t = j + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NHB, PVOFF, PVS>(t);
           return n;
         }();
-        constexpr bool pv = j >= PVOFF && j - PVOFF < NV;
-        constexpr int g = PV0 + (pv ? j - PVOFF : 0), c = g / SPC, j4 = (g % SPC) / NHB, hb = g % NHB;
+        constexpr bool pv = pass_has_pv(j, NV, PVOFF, PVS);
+        constexpr int g = PV0 + (pv ? (j - PVOFF) / PVS : 0), c = g / SPC, j4 = (g % SPC) / NHB, hb = g % NHB;
         constexpr bool has_k = j < NS;
         constexpr bool has_v = pv && hb == 0;
         constexpr bool has_p = pv && j4 == 0;
@@ -754,8 +1126,8 @@ void mla_partial_kernel(PartialArgs a) {
       auto owner_iteration = [&]() __attribute__((always_inline)) {
         f32x16 s;
         pass(std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
-             std::integral_constant<int, PV_START>{}, std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s,
-             pass1_hook(std::integral_constant<int, NKC>{}));
+             std::integral_constant<int, PV_START>{}, std::integral_constant<int, PV_STRIDE>{},
+             std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s, pass1_hook(std::integral_constant<int, NKC>{}));
         const bool full = (st_s + 1) * kSubTokens <= n_b;  // no token past the sequence
         const float c = a.qk_scale_log2;
         float m_use = m_run, lsum = 0.0f, alpha = 1.0f;
@@ -805,8 +1177,8 @@ void mla_partial_kernel(PartialArgs a) {
         };
         static_assert(SM_STEPS == 11, "softmax pieces 0..10");
         pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * SPC>{},
-             std::integral_constant<int, 0>{}, std::integral_constant<int, SM_STEPS>{}, kst_v, kst_r, vst, pst, s,
-             softmax_hook);
+             std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, std::integral_constant<int, SM_STEPS>{},
+             kst_v, kst_r, vst, pst, s, softmax_hook);
         {
           char LDS_AS* pw = lds + OFF_P + (pbuf ^ 1) * PSLOT + wave * 2 * 1024 + lane * 16;
           ds_write_b128<0>(pw, pnext[0]);
@@ -822,11 +1194,11 @@ void mla_partial_kernel(PartialArgs a) {
       auto pv_iteration = [&]() __attribute__((always_inline)) {
         f32x16 s;
         pass(std::false_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
-             std::integral_constant<int, PV_START>{}, std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s,
-             pass1_hook(std::integral_constant<int, PV_SPLIT + PV_START>{}));
+             std::integral_constant<int, PV_START>{}, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{},
+             kst_v, kst_r, vst, pst, s, pass1_hook(std::integral_constant<int, PV_SPLIT + PV_START>{}));
         pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * SPC>{},
-             std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s,
-             [](auto) {});
+             std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{},
+             kst_v, kst_r, vst, pst, s, [](auto) {});
       };
       if constexpr (NHB == NW) {
         owner_iteration();
@@ -912,7 +1284,7 @@ void mla_partial_kernel(PartialArgs a) {
           if (seg.direct)
             a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
           else
-            a.mid_lse[(int64_t)seg.slot * a.num_heads + head] = lse2;
+            store_through_f32(a.mid_lse + (int64_t)seg.slot * a.num_heads + head, lse2);
         }
         // the next segment refills the rings
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -920,10 +1292,30 @@ void mla_partial_kernel(PartialArgs a) {
       }
     }
 
+    if (a.fused && !seg.direct) {
+      // every wave's write-through partial row and lse stores have
+      // completed before the arrival
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();
+      if (wave == 0 && lane == 0) {
+        const int old = sys_add(a.m_count + (int64_t)b * gridDim.y + blockIdx.y, 1);
+        int* r = s_pend[b == b_first ? 0 : 1];
+        r[4] = old == r[2] - 1;  // this arrival completed the count
+      }
+    }
+
     remaining -= (t_end - t_start);
     seg_global_off += nt_b;
     ++b;
     t_start = 0;
+  }
+
+  if (a.fused) {
+    const CoherentLoads ld{
+        __builtin_amdgcn_make_buffer_rsrc(a.mid_o, 0, a.mid_o_bytes, kBufferWord3),
+        __builtin_amdgcn_make_buffer_rsrc(a.mid_lse, 0, a.mid_o_bytes / 256, kBufferWord3)};
+    fused_merge_tail<DT>(MergeView{a.mid_o, a.mid_lse, a.num_heads, a.out, a.out_sb, a.out_sh, a.lse}, ld,
+                         a.m_count, a.m_done, a.m_flag, a.spin_limit, wave, s_pend, s_msg, NHB);
   }
 }
 
@@ -975,76 +1367,17 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
     }
   }
   if (head >= a.num_heads || count == 1) return;  // count == 1: written by stage 1
-
-  short* orow = reinterpret_cast<short*>(a.out) + (int64_t)b * a.out_sb + (int64_t)head * a.out_sh;
-  if (count == 0) {  // empty sequence: out = 0, lse = -inf (kernel.py:126-128, 178-181)
-    for (int d = lane * 8; d < DV; d += 512) *reinterpret_cast<i16x8*>(orow + d) = (i16x8)0;
-    if (lane == 0) a.lse[(int64_t)b * a.num_heads + head] = -INFINITY;
-    return;
-  }
   static_assert(DV == 512, "one row = 64 lanes x 8 elements");
-  // Up to 16 splits (the common case): every lse and partial row is
-  // requested at once, then m = max lse2 (-inf -> 0), w = 2^(lse2 - m).
-  // Slots past `count` repeat the last written row with weight 0.
-  constexpr int BATCH = 8;
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  float wsum = 0.0f, m = -INFINITY;
-  auto merge_at_once = [&](auto NC) __attribute__((always_inline)) {
-    constexpr int N = decltype(NC)::value;
-    float l[N];
-    i16x8 v[N];
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const int64_t row = (int64_t)(slot0 + min(j, count - 1)) * a.num_heads + head;
-      l[j] = a.mid_lse[row];
-      v[j] = *reinterpret_cast<const i16x8*>(a.mid_o + row * DV + lane * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < N; ++j)
-      if (j < count) m = fmaxf(m, l[j]);
-    if (m == -INFINITY) m = 0.0f;
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const float w = j < count ? fast_exp2(l[j] - m) : 0.0f;
-      wsum += w;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += w * Elt<DT>::to_float(v[j][e]);
-    }
-  };
-  if (count <= BATCH) {
-    merge_at_once(std::integral_constant<int, BATCH>{});
-  } else if (count <= 2 * BATCH) {
-    merge_at_once(std::integral_constant<int, 2 * BATCH>{});
-  } else {
-    for (int s = lane; s < count; s += 64)
-      m = fmaxf(m, a.mid_lse[(int64_t)(slot0 + s) * a.num_heads + head]);
-    for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
-    if (m == -INFINITY) m = 0.0f;
-    // eight partial rows in flight per batch
-    for (int s0 = 0; s0 < count; s0 += BATCH) {
-      float w[BATCH];
-      i16x8 v[BATCH];
-#pragma unroll
-      for (int j = 0; j < BATCH; ++j) {
-        const int sj = s0 + j;
-        const int64_t row = (int64_t)(slot0 + min(sj, count - 1)) * a.num_heads + head;
-        w[j] = sj < count ? fast_exp2(a.mid_lse[row] - m) : 0.0f;
-        v[j] = *reinterpret_cast<const i16x8*>(a.mid_o + row * DV + lane * 8);
-      }
-#pragma unroll
-      for (int j = 0; j < BATCH; ++j) {
-        wsum += w[j];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += w[j] * Elt<DT>::to_float(v[j][e]);
-      }
-    }
-  }
-  const float inv = wsum > 0.0f ? 1.0f / wsum : 1.0f;
-  i16x8 o;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = Elt<DT>::from_float(acc[e] * inv);
-  *reinterpret_cast<i16x8*>(orow + lane * 8) = o;
-  if (lane == 0) a.lse[(int64_t)b * a.num_heads + head] = wsum > 0.0f ? (m + fast_log2(wsum)) * kLn2 : -INFINITY;
+  const MergeView mv{a.mid_o, a.mid_lse, a.num_heads, a.out, a.out_sb, a.out_sh, a.lse};
+  const PlainLoads ld{a.mid_o, a.mid_lse};
+  if (count == 0)
+    merge_zero(mv, b, head, lane);
+  else if (count <= 8)
+    merge_rows_at_once<DT, 1, 8>(mv, ld, b, head, 1, slot0, count, lane);
+  else if (count <= 16)
+    merge_rows_at_once<DT, 1, 16>(mv, ld, b, head, 1, slot0, count, lane);
+  else
+    merge_row_loop<DT>(mv, ld, b, head, slot0, count, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1063,12 +1396,50 @@ int hip_fail(hipError_t e, const char* where) {
   return TMLA_ERR_HIP;
 }
 
-size_t workspace_bytes(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
-  if (batch < 0 || heads < 0 || dv < 0) return 0;
+// Workgroups per worker along the heads (32, 64 or 128 heads each).
+int head_blocks(int32_t heads) {
+  const int per = heads <= 32 ? 32 : heads <= 64 ? 64 : 128;
+  return (heads + per - 1) / per;
+}
+
+// Workspace: partial rows [slots, H, dv] (input dtype), their base-2 lse
+// [slots, H] (float), then the fused merge's int32 counters m_count and
+// m_done [batch, head blocks] and flags m_flag [slots, head blocks].
+struct WsLayout {
+  size_t o, l, cnt, done, flag, total;  // byte offsets and size
+};
+
+WsLayout ws_layout(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
+  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
   const int64_t slots = splits > 0 ? (int64_t)batch * splits : (int64_t)workers + batch;
-  const size_t o = (size_t)slots * heads * dv * 2;  // partials in the input dtype
-  const size_t l = (size_t)slots * heads * sizeof(float);
-  return ((o + 255) & ~(size_t)255) + l;
+  const int64_t gy = head_blocks(heads);
+  WsLayout w;
+  w.o = 0;
+  w.l = al((size_t)slots * heads * dv * 2);
+  w.cnt = w.l + al((size_t)slots * heads * sizeof(float));
+  w.done = w.cnt + (size_t)batch * gy * 4;
+  w.flag = w.done + (size_t)batch * gy * 4;
+  w.total = w.flag + (size_t)slots * gy * 4;
+  return w;
+}
+
+size_t workspace_bytes(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
+  if (batch < 0 || heads <= 0 || dv < 0) return 0;
+  return ws_layout(batch, heads, dv, splits, workers).total;
+}
+
+int g_spin_limit = 1 << 14;  // polls (about 2^7 clocks each) before a share is handed over
+
+// Compute units of the current device, cached.
+int current_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cache[dev] = n;
+  return n;
 }
 
 struct Common {
@@ -1129,13 +1500,18 @@ int32_t tmla_device_cu_count(int32_t device) {
   return n;
 }
 
-int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
-                            int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
-                            const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols,
-                            const int32_t* seqlens, int32_t batch, int32_t num_heads, int32_t head_dim_v,
-                            int32_t rope_dim, int32_t dtype, float softmax_scale, int32_t num_splits,
-                            int32_t num_workers, void* out, int64_t out_stride_b, int64_t out_stride_h,
-                            float* lse, void* workspace, size_t workspace_bytes_, void* stream) {
+}  // extern "C"
+
+namespace tmla {
+
+// mode 0: stage 1 only; 1: stage 1 with the fused merge when every
+// workgroup fits on the device at once, else both stages; 2: both stages.
+int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv, int64_t kv_stride_0,
+                  int64_t kv_stride_1, int64_t num_blocks, int32_t page_size, const int32_t* block_table,
+                  int64_t bt_stride_b, int32_t bt_cols, const int32_t* seqlens, int32_t batch, int32_t num_heads,
+                  int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale, int32_t num_splits,
+                  int32_t num_workers, void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
+                  void* workspace, size_t workspace_bytes_, void* stream, int mode) {
   const Common c{batch, num_heads, head_dim_v, rope_dim, dtype, num_splits, num_workers};
   int rc = check_common(c, workspace, workspace_bytes_);
   if (rc != TMLA_OK) return rc;
@@ -1181,15 +1557,24 @@ int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_
   a.out_sh = out_stride_h;
   a.lse = lse;
   char* ws = static_cast<char*>(workspace);
-  const int64_t slots = num_splits > 0 ? (int64_t)batch * num_splits : (int64_t)num_workers + batch;
-  a.mid_o = reinterpret_cast<short*>(ws);
-  a.mid_lse = reinterpret_cast<float*>(ws + (((size_t)slots * num_heads * 512 * 2 + 255) & ~(size_t)255));
+  const WsLayout wl = ws_layout(batch, num_heads, 512, num_splits, num_workers);
+  a.mid_o = reinterpret_cast<short*>(ws + wl.o);
+  a.mid_lse = reinterpret_cast<float*>(ws + wl.l);
+  a.m_count = reinterpret_cast<int32_t*>(ws + wl.cnt);
+  a.m_done = reinterpret_cast<int32_t*>(ws + wl.done);
+  a.m_flag = reinterpret_cast<int32_t*>(ws + wl.flag);
+  a.spin_limit = g_spin_limit;
 
   // blocks of 32 heads per workgroup (4 waves in every case)
   const int nhb = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
   const int heads_per_wg = 32 * nhb;
   const int workers = num_splits > 0 ? batch * num_splits : num_workers;
   dim3 grid(workers, (num_heads + heads_per_wg - 1) / heads_per_wg);
+  // The fused merge: one workgroup per compute unit at most (the kernel's LDS
+  // use admits one), so that siblings normally run side by side.
+  const size_t mid_o_bytes = wl.l - wl.o;  // partial rows, 256-byte aligned
+  a.mid_o_bytes = (int32_t)(mid_o_bytes < (size_t)INT32_MAX ? mid_o_bytes : 0);
+  a.fused = mode == 1 && (int64_t)grid.x * grid.y <= current_cu_count() && mid_o_bytes < (size_t)INT32_MAX ? 1 : 0;
   // one page per 32-token sub-tile (sub-tiles never straddle a page) and a
   // power-of-two page size: page slots and in-page rows by shifts and masks
   const bool uni = paged && (page_size % kSubTokens == 0) && a.page_shift >= 0;
@@ -1197,7 +1582,27 @@ int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_
   hipError_t e = dtype == TMLA_BF16 ? launch_partial_dt<TMLA_BF16>(a, grid, nhb, s, paged, uni)
                                     : launch_partial_dt<TMLA_FP16>(a, grid, nhb, s, paged, uni);
   if (e != hipSuccess) return hip_fail(e, "mla_partial_kernel launch");
+  if (mode != 0 && !a.fused)
+    return tmla_mla_decode_combine(seqlens, batch, num_heads, head_dim_v, dtype, num_splits, num_workers, out,
+                                   out_stride_b, out_stride_h, lse, workspace, workspace_bytes_, stream);
   return TMLA_OK;
+}
+
+}  // namespace tmla
+
+extern "C" {
+
+int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                            int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
+                            const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols,
+                            const int32_t* seqlens, int32_t batch, int32_t num_heads, int32_t head_dim_v,
+                            int32_t rope_dim, int32_t dtype, float softmax_scale, int32_t num_splits,
+                            int32_t num_workers, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                            float* lse, void* workspace, size_t workspace_bytes_, void* stream) {
+  return decode_launch(q, q_stride_b, q_stride_h, kv, kv_stride_0, kv_stride_1, num_blocks, page_size, block_table,
+                       bt_stride_b, bt_cols, seqlens, batch, num_heads, head_dim_v, rope_dim, dtype, softmax_scale,
+                       num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace, workspace_bytes_,
+                       stream, 0);
 }
 
 int tmla_mla_decode_combine(const int32_t* seqlens, int32_t batch, int32_t num_heads, int32_t head_dim_v,
@@ -1220,9 +1625,9 @@ int tmla_mla_decode_combine(const int32_t* seqlens, int32_t batch, int32_t num_h
   a.out_sh = out_stride_h;
   a.lse = lse;
   const char* ws = static_cast<const char*>(workspace);
-  const int64_t slots = num_splits > 0 ? (int64_t)batch * num_splits : (int64_t)num_workers + batch;
-  a.mid_o = reinterpret_cast<const short*>(ws);
-  a.mid_lse = reinterpret_cast<const float*>(ws + (((size_t)slots * num_heads * 512 * 2 + 255) & ~(size_t)255));
+  const WsLayout wl = ws_layout(batch, num_heads, 512, num_splits, num_workers);
+  a.mid_o = reinterpret_cast<const short*>(ws + wl.o);
+  a.mid_lse = reinterpret_cast<const float*>(ws + wl.l);
   dim3 grid(batch, (num_heads + 3) / 4);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TMLA_BF16)
@@ -1240,13 +1645,28 @@ int tmla_mla_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
                     int32_t num_heads, int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale,
                     int32_t num_splits, int32_t num_workers, void* out, int64_t out_stride_b,
                     int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes_, void* stream) {
-  int rc = tmla_mla_decode_partial(q, q_stride_b, q_stride_h, kv, kv_stride_0, kv_stride_1, num_blocks, page_size,
-                                   block_table, bt_stride_b, bt_cols, seqlens, batch, num_heads, head_dim_v,
-                                   rope_dim, dtype, softmax_scale, num_splits, num_workers, out, out_stride_b,
-                                   out_stride_h, lse, workspace, workspace_bytes_, stream);
-  if (rc != TMLA_OK) return rc;
-  return tmla_mla_decode_combine(seqlens, batch, num_heads, head_dim_v, dtype, num_splits, num_workers, out,
-                                 out_stride_b, out_stride_h, lse, workspace, workspace_bytes_, stream);
+  return decode_launch(q, q_stride_b, q_stride_h, kv, kv_stride_0, kv_stride_1, num_blocks, page_size, block_table,
+                       bt_stride_b, bt_cols, seqlens, batch, num_heads, head_dim_v, rope_dim, dtype, softmax_scale,
+                       num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace, workspace_bytes_,
+                       stream, 2);
+}
+
+int tmla_mla_decode_fused(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv, int64_t kv_stride_0,
+                          int64_t kv_stride_1, int64_t num_blocks, int32_t page_size, const int32_t* block_table,
+                          int64_t bt_stride_b, int32_t bt_cols, const int32_t* seqlens, int32_t batch,
+                          int32_t num_heads, int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale,
+                          int32_t num_splits, int32_t num_workers, void* out, int64_t out_stride_b,
+                          int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes_, void* stream) {
+  return decode_launch(q, q_stride_b, q_stride_h, kv, kv_stride_0, kv_stride_1, num_blocks, page_size, block_table,
+                       bt_stride_b, bt_cols, seqlens, batch, num_heads, head_dim_v, rope_dim, dtype, softmax_scale,
+                       num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace, workspace_bytes_,
+                       stream, 1);
+}
+
+int32_t tmla_set_merge_spin_limit(int32_t polls) {
+  const int32_t prev = g_spin_limit;
+  if (polls >= 0) g_spin_limit = polls;
+  return prev;
 }
 
 }  // extern "C"

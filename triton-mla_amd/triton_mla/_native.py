@@ -24,12 +24,16 @@ SIGNATURES = {
     "tmla_version": (ctypes.c_int, []),
     "tmla_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "tmla_device_cu_count": (_i32, [_i32]),
+    "tmla_set_merge_spin_limit": (_i32, [_i32]),
     "tmla_mla_decode_partial": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
         _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "tmla_mla_decode_combine": (ctypes.c_int, [
         _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "tmla_mla_decode": (ctypes.c_int, [
+        _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
+        _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "tmla_mla_decode_fused": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
         _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "tmla_mla_absorb_q": (ctypes.c_int, [

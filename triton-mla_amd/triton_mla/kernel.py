@@ -69,7 +69,7 @@ class DecodeLaunch:
     """
 
     def __init__(self, q, kv_cache, cache_seqlens, block_table=None, head_dim_v=512,
-                 softmax_scale=None, num_splits=None):
+                 softmax_scale=None, num_splits=None, num_workers=None):
         # validation mirrors kernel.py:235-245
         if kv_cache.dim() == 4:
             assert kv_cache.shape[2] == 1, "MLA uses a single shared latent KV head"
@@ -117,6 +117,7 @@ class DecodeLaunch:
         self.batch, self.num_heads, self.head_dim_v, self.d_rope = batch, num_heads, head_dim_v, d_rope
         self.out = torch.empty(batch, num_heads, head_dim_v, dtype=q.dtype, device=device)
         self.lse = torch.empty(batch, num_heads, dtype=torch.float32, device=device)
+        self.fused = False
         if batch == 0:
             return
         if num_blocks == 0:
@@ -129,9 +130,17 @@ class DecodeLaunch:
         self._keep = (q, kv_cache, cache_seqlens, block_table)
         self.lib = _native.load()
         self.splits = num_splits if num_splits is not None else 0
-        self.workers = 0 if num_splits is not None else _num_sms(device)
+        # balanced partition: one worker per compute unit unless asked otherwise
+        self.workers = 0 if num_splits is not None else int(num_workers or _num_sms(device))
         self.ws_bytes = self.lib.tmla_workspace_bytes(batch, num_heads, head_dim_v, self.splits, self.workers)
-        self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=device)
+        # zero-filled once: the fused merge's counters start at zero and every
+        # call leaves them at zero
+        self.workspace = torch.zeros(max(self.ws_bytes, 1), dtype=torch.uint8, device=device)
+        # run(single_launch=True) merges inside the partial kernel (one launch)
+        # when all of its workgroups fit on the device at once, one per CU
+        per_wg = 32 if num_heads <= 32 else 64 if num_heads <= 64 else 128
+        grid = (batch * self.splits if self.splits else self.workers) * -(-num_heads // per_wg)
+        self.fused = grid <= _num_sms(device)
         self._partial_args = (
             q.data_ptr(), q.stride(0), q.stride(1),
             kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), num_blocks, page_size,
@@ -161,12 +170,13 @@ class DecodeLaunch:
                 _native.check(self.lib.tmla_mla_decode_combine(*self._combine_args, self._stream()),
                               "tmla_mla_decode_combine")
 
-    def run(self):
-        """Both stages (tmla_mla_decode)."""
+    def run(self, single_launch=False):
+        """Both stages (tmla_mla_decode), or the single-launch form
+        (tmla_mla_decode_fused) when single_launch is set."""
         if self.batch:
+            name = "tmla_mla_decode_fused" if single_launch else "tmla_mla_decode"
             with torch.cuda.device(self.device):
-                _native.check(self.lib.tmla_mla_decode(*self._partial_args, self._stream()),
-                              "tmla_mla_decode")
+                _native.check(getattr(self.lib, name)(*self._partial_args, self._stream()), name)
         return self.out, self.lse
 
 
@@ -179,6 +189,7 @@ def mla_decode(
     softmax_scale: float = None,
     num_splits: int = None,
     return_lse: bool = False,
+    single_launch: bool = False,
 ):
     """Weight-absorbed MLA decode attention over a shared latent KV cache.
 
@@ -197,13 +208,16 @@ def mla_decode(
             host sync, graph-capturable). An int cuts every sequence into that
             many tile-aligned pieces, as the reference's split-KV scheme does.
         return_lse: also return the natural-log log-sum-exp per head.
+        single_launch: merge the split partials inside the partial kernel
+            (one launch instead of two, same bits) when its workgroups fit on
+            the device at once.
 
     Returns:
         out [batch, num_heads, head_dim_v] in q.dtype (and lse [batch,
         num_heads] float32).
     """
     call = DecodeLaunch(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits)
-    out, lse = call.run()
+    out, lse = call.run(single_launch)
     if return_lse:
         return out, lse
     return out
