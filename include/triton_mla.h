@@ -142,6 +142,32 @@ int tmla_mla_decode_fused(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes,
                           void* stream);
 
+/*
+ * Multi-token (causal) decode, no counterpart in the reference (its
+ * `mla_decode` takes one query token per sequence: kernel.py:238 asserts a
+ * 3-D q, README.md:32 "single-token decode only"). For speculative decoding
+ * and chunked prefill onto the cache: each sequence b has q_len query tokens,
+ * the last q_len of its cache_seqlens[b] tokens, and query token t sees the
+ * first cache_seqlens[b] - (q_len - 1 - t) tokens (none when that is <= 0:
+ * out = 0, lse = -inf).
+ *   q    [batch, q_len * num_heads, head_dim_v + rope_dim]: row t * num_heads
+ *        + h of sequence b at q + b * q_stride_b + (t * num_heads + h) *
+ *        q_stride_h (a [batch, q_len, num_heads, D] tensor whose token and
+ *        head dims are packed).
+ *   out  [batch, q_len * num_heads, head_dim_v] the same way; lse [batch,
+ *        q_len * num_heads] float32 natural log.
+ * The workspace is tmla_workspace_bytes(batch, q_len * num_heads, ...).
+ * single_launch != 0 runs like tmla_mla_decode_fused, else like
+ * tmla_mla_decode. q_len = 1 gives tmla_mla_decode's results bit for bit.
+ */
+int tmla_mla_decode_causal(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                           int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks,
+                           int32_t page_size, const int32_t* block_table, int64_t bt_stride_b,
+                           int32_t bt_cols, const int32_t* seqlens, int32_t batch, int32_t q_len,
+                           int32_t num_heads, int32_t head_dim_v, int32_t rope_dim, int32_t dtype,
+                           float softmax_scale, int32_t num_splits, int32_t num_workers, void* out,
+                           int64_t out_stride_b, int64_t out_stride_h, float* lse, void* workspace,
+                           size_t workspace_bytes, int32_t single_launch, void* stream);
 /* Number of compute units of `device` (0 on error); the default worker count. */
 int32_t tmla_device_cu_count(int32_t device);
 

@@ -10,6 +10,8 @@ Contents
   reference's ``gather_kv`` / ``mla_decode_ref`` (src/triton_mla/reference.py:6-31),
   ``get_num_splits`` (src/triton_mla/kernel.py:190-201) and the fused
   kernel's split/merge algebra (kernel.py:83-86, 119-128, 165-181));
+* ``mla_decode_ref_causal``: multi-token causal decode built on the
+  single-token oracle (an extension; no reference counterpart);
 * a numpy float64 restatement of the ``MLA`` layer (src/triton_mla/model.py):
   RMSNorm (model.py:34-41), rotate-half RoPE (model.py:44-50), projections
   (model.py:74-82), cache append (model.py:84-94), ``W_UK``/``W_UV`` split
@@ -138,6 +140,32 @@ def mla_decode_ref(q, kv_cache, cache_seqlens, block_table=None, head_dim_v=512,
         _ptr(out), _ptr(lse))
     if rc != 0:
         raise RuntimeError(f"oracle_mla_decode_ref failed ({rc})")
+    return out, lse
+
+
+def mla_decode_ref_causal(q, kv_cache, cache_seqlens, block_table=None, head_dim_v=512,
+                          softmax_scale=None, dtype="bf16", nthreads=0):
+    """Multi-token causal decode, a float64 oracle for an extension with no
+    counterpart in the reference (its mla_decode takes one query token,
+    src/triton_mla/kernel.py:238).
+
+    q is [B, T, H, D]: the T query tokens of sequence b are its last T cached
+    tokens, and query token t attends to the first
+    max(cache_seqlens[b] - (T - 1 - t), 0) tokens. Each token is therefore the
+    single-token oracle (reference.py:16-31) with that length.
+    Returns ``(out float32 [B, T, H, dv], lse float32 [B, T, H])``.
+    """
+    q = _u16(q)
+    B, T, H, D = q.shape
+    seqlens = np.asarray(cache_seqlens, dtype=np.int64)
+    out = np.empty((B, T, H, head_dim_v), dtype=np.float32)
+    lse = np.empty((B, T, H), dtype=np.float32)
+    for t in range(T):
+        n_t = np.maximum(seqlens - (T - 1 - t), 0).astype(np.int32)
+        o, l = mla_decode_ref(np.ascontiguousarray(q[:, t]), kv_cache, n_t, block_table, head_dim_v,
+                              softmax_scale, dtype, nthreads)
+        out[:, t] = o
+        lse[:, t] = l
     return out, lse
 
 

@@ -176,6 +176,39 @@ def test_decode_ref_paging_and_token_order_invariance():
     np.testing.assert_allclose(a[1], c[1], rtol=1e-6, atol=1e-7)
 
 
+def test_causal_ref_matches_masked_softmax():
+    """Multi-token causal oracle against an explicit [T, N] visibility mask and
+    scipy's softmax/logsumexp over the whole score matrix (a different
+    computation from the per-token truncation the oracle uses), including a
+    sequence shorter than q_len (query tokens that see nothing: out 0, lse -inf)."""
+    rng = np.random.default_rng(11)
+    T, H, page = 3, 4, 8
+    n = np.array([13, 2, 8], np.int32)
+    B = len(n)
+    pages = 2
+    q = rand_bits(rng, (B, T, H, D))
+    kv = rand_bits(rng, (B * pages, page, D))
+    bt = rng.permutation(B * pages).astype(np.int32).reshape(B, pages)
+    out, lse = oracle.mla_decode_ref_causal(q, kv, n, bt, DV, 0.06)
+    qf, kf = as_f64(q), as_f64(kv)
+    for b in range(B):
+        toks = kf[bt[b]].reshape(pages * page, D)[: n[b]]
+        s = np.einsum("thd,nd->thn", qf[b], toks) * 0.06
+        # token t (the (n - T + t)-th cached token) sees positions j <= n - T + t
+        vis = np.arange(n[b])[None, :] <= (n[b] - T + np.arange(T))[:, None]
+        for t in range(T):
+            if not vis[t].any():
+                assert np.all(out[b, t] == 0) and np.all(np.isneginf(lse[b, t]))
+                continue
+            st = np.where(vis[t][None, :], s[t], -np.inf)
+            np.testing.assert_allclose(lse[b, t], logsumexp(st, axis=-1), rtol=1e-6, atol=1e-6)
+            np.testing.assert_allclose(out[b, t], softmax(st, axis=-1) @ toks[:, :DV], rtol=1e-5, atol=1e-6)
+    # one query token is the single-token oracle
+    o1, l1 = oracle.mla_decode_ref_causal(q[:, :1], kv, n, bt, DV, 0.06)
+    r1 = oracle.mla_decode_ref(q[:, 0], kv, n, bt, DV, 0.06)
+    assert np.array_equal(o1[:, 0], r1[0]) and np.array_equal(l1[:, 0], r1[1])
+
+
 def test_split_merge_matches_direct():
     """The fused kernel's split/merge algebra equals direct attention for any split count."""
     rng = np.random.default_rng(5)

@@ -41,9 +41,27 @@ namespace tmla {
 
 constexpr int kTileTokens = 64;     // planning unit (one page at page_size 64)
 constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
+// Schedule of the partial kernel's tile loop (build-time knobs): LDS operand
+// reads issued this many MFMA steps ahead of their use; PV MFMAs beside the
+// S chain, in units of NHB of the 2 * 4 * NHB PV MFMAs of a sub-tile (the
+// rest run beside the softmax); the spacing of those PV MFMAs among the S
+// steps; exponentials per step of the softmax pass.
+#ifndef TMLA_READ_AHEAD
+#define TMLA_READ_AHEAD 2
+#endif
+#ifndef TMLA_PV1_EIGHTHS
+#define TMLA_PV1_EIGHTHS 4
+#endif
+#ifndef TMLA_PV_STRIDE
+#define TMLA_PV_STRIDE 2
+#endif
+#ifndef TMLA_EXP_PER_STEP
+#define TMLA_EXP_PER_STEP 2
+#endif
 constexpr int kStages = 4;          // LDS ring depth (3 sub-tiles in flight)
 constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (p <= 2^8)
+constexpr float kNoMax = -__FLT_MAX__;  // running max of a head that has seen no token
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -60,6 +78,10 @@ struct PartialArgs {
   int32_t bt_cols;
   const int32_t* seqlens;
   int32_t batch, num_heads;
+  // Multi-token queries: head index v = t * heads_per_token + h for query
+  // token t < q_len, which sees the first seqlen - (q_len - 1 - t) tokens
+  // (q_len = 1: single-token decode, every head sees seqlen tokens).
+  int32_t q_len, heads_per_token;
   float qk_scale_log2;
   int32_t num_splits, num_workers;
   int32_t xcds;            // workgroups are dealt round-robin over this many L2 domains
@@ -107,6 +129,12 @@ __device__ __forceinline__ int lane_id_fresh() {
   int v;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(v));
   return v;
+}
+
+// Tokens at the end of the sequence that query head `head` does not see:
+// q_len - 1 - t for the head's query token t (0 for single-token decode).
+__device__ __forceinline__ int causal_lag(const PartialArgs& a, int head) {
+  return a.q_len <= 1 ? 0 : a.q_len - 1 - min(head, a.num_heads - 1) / a.heads_per_token;
 }
 
 // Register-class pins: an empty asm that requires its operand in VGPRs /
@@ -647,6 +675,8 @@ void mla_partial_kernel(PartialArgs a) {
                          : (int)blockIdx.x;
   const bool s_owner = NHB == 4 || wave < NHB;  // runs S and the softmax of head block `wave`
   const int head_base = blockIdx.y * (kHeadsPerWave * NHB) + wave * kHeadsPerWave;
+  // the wave's first head has its earliest query token: the most tokens unseen
+  const int lag_wave = __builtin_amdgcn_readfirstlane(causal_lag(a, head_base));
   // fused merge: this worker clears sequences worker, worker + nwg, ... when
   // they are empty; the first length is requested now, used at the end
   const int pre_len = __builtin_amdgcn_readfirstlane((a.fused && worker < a.batch) ? a.seqlens[worker] : 1);
@@ -816,7 +846,9 @@ void mla_partial_kernel(PartialArgs a) {
     f32x16 acc[NACC];
 #pragma unroll
     for (int d = 0; d < NACC; ++d) acc[d] = (f32x16)0.0f;
-    float m_run = -INFINITY;  // base-2 reference max (per head)
+    // base-2 reference max (per head); kNoMax until the head has seen a token,
+    // so that p = exp2(s * c - m) of a masked score (s = -inf) is 0 even then
+    float m_run = kNoMax;
     float l_run = 0.0f;       // sum of p over this lane's half of the tokens
     i16x8 qop[NKC];           // Q^T operands (B of S^T = K . Q^T), loaded below
     i16x8 pop[2][NHB];        // P^T operands of the sub-tile in PV: [c][hb]
@@ -902,15 +934,19 @@ void mla_partial_kernel(PartialArgs a) {
     // after its own. hook(step) runs after each step's MFMAs (copies of a
     // later sub-tile, the rescale check, softmax pieces), so its VALU and
     // memory work overlaps them.
-    constexpr int PD = 2;
+    constexpr int PD = TMLA_READ_AHEAD;
     constexpr int SPC = NDBW * NHB;    // PV steps per token half
-    constexpr int PV_SPLIT = SPC;      // token half 0 beside S, half 1 beside the softmax
+    // PV steps beside S (pass 1); the rest run beside the softmax (pass 2)
+    constexpr int PV_SPLIT = NHB * TMLA_PV1_EIGHTHS;
     constexpr int PV_START = 4;        // S-only steps first: the rescale factors arrive meanwhile
-    constexpr int SM_STEPS = 11;       // steps the softmax pieces need in pass 2
+    constexpr int EXP_PER_STEP = TMLA_EXP_PER_STEP;
+    constexpr int SM_STEPS = 3 + 16 / EXP_PER_STEP;  // steps the softmax pieces need in pass 2
+    static_assert(PV_SPLIT > 0 && PV_SPLIT <= 2 * SPC && 16 % EXP_PER_STEP == 0, "schedule");
     // pass 1 of an S wave: one PV step every PV_STRIDE S steps, so that the
     // time between a read and its use (PD steps) never shrinks to PD bare S
     // steps
-    constexpr int PV_STRIDE = 2;
+    constexpr int PV_STRIDE0 = (NKC - 1 - PV_START) / (PV_SPLIT > 1 ? PV_SPLIT - 1 : 1);
+    constexpr int PV_STRIDE = TMLA_PV_STRIDE < PV_STRIDE0 ? TMLA_PV_STRIDE : (PV_STRIDE0 > 0 ? PV_STRIDE0 : 1);
     static_assert(NDBW == 4, "four 32-dim blocks per wave");
     auto pass = [&](auto DOS, auto PVLO, auto PVHI, auto PVOFFC, auto PVSC, auto MINSTEPS, const char LDS_AS* kst_v,
                     const char LDS_AS* kst_r, const char LDS_AS* vst, const char LDS_AS* pst, f32x16& s, auto&& hook)
@@ -1128,7 +1164,8 @@ void mla_partial_kernel(PartialArgs a) {
         pass(std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
              std::integral_constant<int, PV_START>{}, std::integral_constant<int, PV_STRIDE>{},
              std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s, pass1_hook(std::integral_constant<int, NKC>{}));
-        const bool full = (st_s + 1) * kSubTokens <= n_b;  // no token past the sequence
+        // no token past the sequence (for the wave's earliest query token)
+        const bool full = (st_s + 1) * kSubTokens <= n_b - lag_wave;
         const float c = a.qk_scale_log2;
         float m_use = m_run, lsum = 0.0f, alpha = 1.0f;
         i16x8 pnext[2];
@@ -1140,7 +1177,7 @@ void mla_partial_kernel(PartialArgs a) {
               const float off = c >= 0.0f ? -INFINITY : INFINITY;
 #pragma unroll
               for (int r = 0; r < 16; ++r)
-                if (tok0 + 8 * (r >> 2) + (r & 3) >= n_b) s[r] = off;
+                if (tok0 + 8 * (r >> 2) + (r & 3) >= n_b - causal_lag(a, head_base + (lane_id_fresh() & 31))) s[r] = off;
             }
             pin_f16(s);
           } else if constexpr (j == 1) {  // reference max
@@ -1158,24 +1195,23 @@ void mla_partial_kernel(PartialArgs a) {
               // counting: let every counted read finish first
               asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
               m_use = fmaxf(m_run, fmaxf(mx, __shfl_xor(mx, 32)));
-              if (m_run != -INFINITY) alpha = fast_exp2(m_run - m_use);
+              if (m_run != kNoMax) alpha = fast_exp2(m_run - m_use);
             }
             pin_f2(m_use, alpha);
-          } else if constexpr (j >= 2 && j < 10) {  // two probabilities
+          } else if constexpr (j >= 2 && j < 2 + 16 / EXP_PER_STEP) {  // EXP_PER_STEP probabilities
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const int r = 2 * (j - 2) + e;
+            for (int e = 0; e < EXP_PER_STEP; ++e) {
+              const int r = EXP_PER_STEP * (j - 2) + e;
               s[r] = fast_exp2(fmaf(s[r], c, -m_use));  // masked: +-inf * c = -inf -> 0
               lsum += s[r];
             }
             pin_f16(s);
             pin_f1(lsum);
-          } else if constexpr (j == 10) {
+          } else if constexpr (j == 2 + 16 / EXP_PER_STEP) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) pnext[r >> 3][r & 7] = Elt<DT>::from_float(s[r]);
           }
         };
-        static_assert(SM_STEPS == 11, "softmax pieces 0..10");
         pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * SPC>{},
              std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, std::integral_constant<int, SM_STEPS>{},
              kst_v, kst_r, vst, pst, s, softmax_hook);
@@ -1511,7 +1547,7 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
                   int64_t bt_stride_b, int32_t bt_cols, const int32_t* seqlens, int32_t batch, int32_t num_heads,
                   int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale, int32_t num_splits,
                   int32_t num_workers, void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
-                  void* workspace, size_t workspace_bytes_, void* stream, int mode) {
+                  void* workspace, size_t workspace_bytes_, void* stream, int mode, int32_t q_len = 1) {
   const Common c{batch, num_heads, head_dim_v, rope_dim, dtype, num_splits, num_workers};
   int rc = check_common(c, workspace, workspace_bytes_);
   if (rc != TMLA_OK) return rc;
@@ -1544,6 +1580,9 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   a.seqlens = seqlens;
   a.batch = batch;
   a.num_heads = num_heads;
+  if (q_len < 1 || num_heads % q_len != 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "q_len must be >= 1");
+  a.q_len = q_len;
+  a.heads_per_token = num_heads / q_len;
   // A zero scale (every score 0) runs as the smallest normal float instead:
   // the probabilities then differ from 1 by far less than one ulp, and masked
   // tokens (score -inf) still get exactly 0.
@@ -1661,6 +1700,21 @@ int tmla_mla_decode_fused(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                        bt_stride_b, bt_cols, seqlens, batch, num_heads, head_dim_v, rope_dim, dtype, softmax_scale,
                        num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace, workspace_bytes_,
                        stream, 1);
+}
+
+int tmla_mla_decode_causal(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                           int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
+                           const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols, const int32_t* seqlens,
+                           int32_t batch, int32_t q_len, int32_t num_heads, int32_t head_dim_v, int32_t rope_dim,
+                           int32_t dtype, float softmax_scale, int32_t num_splits, int32_t num_workers, void* out,
+                           int64_t out_stride_b, int64_t out_stride_h, float* lse, void* workspace,
+                           size_t workspace_bytes_, int32_t single_launch, void* stream) {
+  if (q_len < 1 || num_heads <= 0 || (int64_t)q_len * num_heads > INT32_MAX)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "q_len must be >= 1 and q_len * num_heads must fit int32");
+  return decode_launch(q, q_stride_b, q_stride_h, kv, kv_stride_0, kv_stride_1, num_blocks, page_size, block_table,
+                       bt_stride_b, bt_cols, seqlens, batch, q_len * num_heads, head_dim_v, rope_dim, dtype,
+                       softmax_scale, num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace,
+                       workspace_bytes_, stream, single_launch ? 1 : 2, q_len);
 }
 
 int32_t tmla_set_merge_spin_limit(int32_t polls) {

@@ -74,8 +74,21 @@ class DecodeLaunch:
         if kv_cache.dim() == 4:
             assert kv_cache.shape[2] == 1, "MLA uses a single shared latent KV head"
             kv_cache = kv_cache.squeeze(2)
+        # Multi-token queries [batch, q_len, num_heads, D] (an extension: the
+        # reference takes one query token, kernel.py:238): query token t sees
+        # the first cache_seqlens - (q_len - 1 - t) tokens. Token and head
+        # dims are packed into one "virtual head" dim t * num_heads + h.
+        q_len = 1
+        multi_token = q.dim() == 4
+        if multi_token:
+            q_len = q.shape[1]
+            assert q_len >= 1, "q must hold at least one query token"
+            if q.stride(1) != q.shape[2] * q.stride(2):
+                q = q.contiguous()
+            q = q.reshape(q.shape[0], q_len * q.shape[2], q.shape[3])
         assert q.dim() == 3 and kv_cache.dim() == 3
         batch, num_heads, d_qk = q.shape
+        num_heads //= q_len  # heads per query token
         d_rope = d_qk - head_dim_v
         assert kv_cache.shape[-1] == d_qk
         assert q.stride(-1) == 1 and kv_cache.stride(-1) == 1
@@ -115,8 +128,11 @@ class DecodeLaunch:
 
         self.device = device
         self.batch, self.num_heads, self.head_dim_v, self.d_rope = batch, num_heads, head_dim_v, d_rope
-        self.out = torch.empty(batch, num_heads, head_dim_v, dtype=q.dtype, device=device)
-        self.lse = torch.empty(batch, num_heads, dtype=torch.float32, device=device)
+        self.q_len = q_len
+        shape = (batch, q_len, num_heads) if multi_token else (batch, num_heads)
+        self.out = torch.empty(*shape, head_dim_v, dtype=q.dtype, device=device)
+        self.lse = torch.empty(*shape, dtype=torch.float32, device=device)
+        vheads = q_len * num_heads  # rows of q / out per sequence
         self.fused = False
         if batch == 0:
             return
@@ -132,22 +148,26 @@ class DecodeLaunch:
         self.splits = num_splits if num_splits is not None else 0
         # balanced partition: one worker per compute unit unless asked otherwise
         self.workers = 0 if num_splits is not None else int(num_workers or _num_sms(device))
-        self.ws_bytes = self.lib.tmla_workspace_bytes(batch, num_heads, head_dim_v, self.splits, self.workers)
+        self.ws_bytes = self.lib.tmla_workspace_bytes(batch, vheads, head_dim_v, self.splits, self.workers)
         # zero-filled once: the fused merge's counters start at zero and every
         # call leaves them at zero
         self.workspace = torch.zeros(max(self.ws_bytes, 1), dtype=torch.uint8, device=device)
         # run(single_launch=True) merges inside the partial kernel (one launch)
         # when all of its workgroups fit on the device at once, one per CU
-        per_wg = 32 if num_heads <= 32 else 64 if num_heads <= 64 else 128
-        grid = (batch * self.splits if self.splits else self.workers) * -(-num_heads // per_wg)
+        per_wg = 32 if vheads <= 32 else 64 if vheads <= 64 else 128
+        grid = (batch * self.splits if self.splits else self.workers) * -(-vheads // per_wg)
         self.fused = grid <= _num_sms(device)
+        out_sh = self.out.stride(-2)  # one output row per (query token, head)
         self._partial_args = (
             q.data_ptr(), q.stride(0), q.stride(1),
             kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), num_blocks, page_size,
             *bt_args, cache_seqlens.data_ptr(), batch, num_heads, head_dim_v, d_rope,
             _native.DTYPE_CODE[q.dtype], float(softmax_scale), self.splits, self.workers,
-            self.out.data_ptr(), self.out.stride(0), self.out.stride(1), self.lse.data_ptr(),
+            self.out.data_ptr(), self.out.stride(0), out_sh, self.lse.data_ptr(),
             self.workspace.data_ptr(), self.ws_bytes)
+        if q_len > 1:  # the same arguments with q_len before num_heads
+            a = self._partial_args
+            self._causal_args = a[:13] + (q_len,) + a[13:]
         self._combine_args = (
             cache_seqlens.data_ptr(), batch, num_heads, head_dim_v, _native.DTYPE_CODE[q.dtype],
             self.splits, self.workers, self.out.data_ptr(), self.out.stride(0), self.out.stride(1),
@@ -158,6 +178,8 @@ class DecodeLaunch:
 
     def partial(self):
         """Stage 1 on the current stream (tmla_mla_decode_partial)."""
+        if self.q_len > 1:
+            raise NotImplementedError("multi-token queries run both stages at once (run())")
         if self.batch:
             with torch.cuda.device(self.device):
                 _native.check(self.lib.tmla_mla_decode_partial(*self._partial_args, self._stream()),
@@ -165,6 +187,8 @@ class DecodeLaunch:
 
     def combine(self):
         """Stage 2 on the current stream (tmla_mla_decode_combine)."""
+        if self.q_len > 1:
+            raise NotImplementedError("multi-token queries run both stages at once (run())")
         if self.batch:
             with torch.cuda.device(self.device):
                 _native.check(self.lib.tmla_mla_decode_combine(*self._combine_args, self._stream()),
@@ -173,7 +197,11 @@ class DecodeLaunch:
     def run(self, single_launch=False):
         """Both stages (tmla_mla_decode), or the single-launch form
         (tmla_mla_decode_fused) when single_launch is set."""
-        if self.batch:
+        if self.batch and self.q_len > 1:
+            with torch.cuda.device(self.device):
+                _native.check(self.lib.tmla_mla_decode_causal(*self._causal_args, int(bool(single_launch)),
+                                                              self._stream()), "tmla_mla_decode_causal")
+        elif self.batch:
             name = "tmla_mla_decode_fused" if single_launch else "tmla_mla_decode"
             with torch.cuda.device(self.device):
                 _native.check(getattr(self.lib, name)(*self._partial_args, self._stream()), name)
@@ -195,7 +223,12 @@ def mla_decode(
 
     Args:
         q: [batch, num_heads, head_dim_v + rope_dim]; the first head_dim_v dims
-            are the W_UK-absorbed nope query, the rest the RoPE query.
+            are the W_UK-absorbed nope query, the rest the RoPE query. An
+            extension beyond the reference: q of shape [batch, q_len,
+            num_heads, D] holds q_len query tokens per sequence (the last
+            q_len cached tokens, e.g. speculative drafts); query token t
+            attends causally to the first cache_seqlens - (q_len - 1 - t)
+            tokens, and out / lse gain the q_len dim.
         kv_cache: paged [num_blocks, page_size, head_dim_v + rope_dim] when
             block_table is given, otherwise dense [batch, max_seqlen, ...].
             A singleton kv-head dim ([..., 1, D], FlashMLA layout) is accepted.
