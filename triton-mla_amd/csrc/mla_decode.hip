@@ -58,6 +58,10 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 #ifndef TMLA_EXP_PER_STEP
 #define TMLA_EXP_PER_STEP 2
 #endif
+// 1: one LDS wait per two MFMA steps (for the operands of both)
+#ifndef TMLA_WAIT_PAIR
+#define TMLA_WAIT_PAIR 0
+#endif
 constexpr int kStages = 4;          // LDS ring depth (3 sub-tiles in flight)
 constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (p <= 2^8)
@@ -201,6 +205,20 @@ __device__ __forceinline__ void lgkm_tie(i16x8& k, i16x4& vl, i16x4& vh, i16x8& 
     asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(vl), "+v"(vh) : "i"(N));
   else if constexpr (HP)
     asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(p) : "i"(N));
+}
+
+// Tie operands to the preceding wait without waiting again (an empty asm
+// that takes them as read-write, so no use of them moves above it).
+template <bool HK, bool HV, bool HP>
+__device__ __forceinline__ void tie_ops(i16x8& k, i16x4& vl, i16x4& vh, i16x8& p) {
+  if constexpr (HK) asm volatile("" : "+v"(k));
+  if constexpr (HV) asm volatile("" : "+v"(vl), "+v"(vh));
+  if constexpr (HP) asm volatile("" : "+v"(p));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)" : : "i"(N));
 }
 
 // Step t of a pass carries PV step PV0 + (t - PVOFF) / PVS when t >= PVOFF
@@ -1005,8 +1023,29 @@ void mla_partial_kernel(PartialArgs a) {
         constexpr int r = j % (PD + 1);
         // the wait ties the operands read for this step to it (a step that
         // only reuses operands needs none)
-        if constexpr (has_k || has_v || has_p)
-          lgkm_tie<after, has_k, has_v, has_p>(kb[r], vl[vi], vh[vi], pop[c][hb]);
+        if constexpr (!TMLA_WAIT_PAIR) {
+          if constexpr (has_k || has_v || has_p)
+            lgkm_tie<after, has_k, has_v, has_p>(kb[r], vl[vi], vh[vi], pop[c][hb]);
+        } else if constexpr (j % 2 == 0) {
+          // one wait per two steps: the operands of steps j and j + 1
+          constexpr int j2 = j + 1 < NSTEPS ? j + 1 : j;
+          constexpr int after2 = [] {
+            int n = 0;
+            for (int t = j2 + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NHB, PVOFF, PVS>(t);
+            return n;
+          }();
+          constexpr bool pv1 = pass_has_pv(j2, NV, PVOFF, PVS);
+          constexpr int g1 = PV0 + (pv1 ? (j2 - PVOFF) / PVS : 0), c1 = g1 / SPC, j41 = (g1 % SPC) / NHB,
+                        hb1 = g1 % NHB;
+          constexpr bool has_k1 = j2 != j && j2 < NS, has_v1 = j2 != j && pv1 && hb1 == 0,
+                         has_p1 = j2 != j && pv1 && j41 == 0;
+          if constexpr (has_k || has_v || has_p || has_k1 || has_v1 || has_p1) {
+            lgkm_wait<after2>();
+            tie_ops<has_k, has_v, has_p>(kb[r], vl[vi], vh[vi], pop[c][hb]);
+            tie_ops<has_k1, has_v1, has_p1>(kb[j2 % (PD + 1)], vl[c1 * NDBW + j41], vh[c1 * NDBW + j41],
+                                            pop[c1][hb1]);
+          }
+        }
         if constexpr (j < NS) {
           if constexpr (j == 0)
             s = mfma_vgpr_first<DT>(kb[0], qop[0]);
