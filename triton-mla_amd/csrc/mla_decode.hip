@@ -47,7 +47,7 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 // rest run beside the softmax); the spacing of those PV MFMAs among the S
 // steps; exponentials per step of the softmax pass.
 #ifndef TMLA_READ_AHEAD
-#define TMLA_READ_AHEAD 2
+#define TMLA_READ_AHEAD 3
 #endif
 #ifndef TMLA_PV1_EIGHTHS
 #define TMLA_PV1_EIGHTHS 4
@@ -58,9 +58,14 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 #ifndef TMLA_EXP_PER_STEP
 #define TMLA_EXP_PER_STEP 2
 #endif
+// start-up order: 0 = Q and sub-tile 0, then sub-tile 1; 1 = Q, sub-tiles 0
+// and 1, then wait for Q and sub-tile 0; 2 = sub-tile 0, Q, sub-tile 1
+#ifndef TMLA_STARTUP
+#define TMLA_STARTUP 1
+#endif
 // 1: one LDS wait per two MFMA steps (for the operands of both)
 #ifndef TMLA_WAIT_PAIR
-#define TMLA_WAIT_PAIR 0
+#define TMLA_WAIT_PAIR 1
 #endif
 constexpr int kStages = 4;          // LDS ring depth (3 sub-tiles in flight)
 constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
@@ -1101,21 +1106,43 @@ void mla_partial_kernel(PartialArgs a) {
 #pragma unroll
       for (int i = 0; i < kStages; ++i) pro_page[i] = page_fetch(st0 + min(i, nst - 1));
     }
-    if (s_owner) {  // only the S waves use Q
-      // heads past num_heads (a partial last block) run on head 0's row:
-      // their scores stay finite and their output rows are never stored
-      const short* qrow = reinterpret_cast<const short*>(a.q) + (int64_t)b * a.q_sb +
-                          (int64_t)(head_ok ? head : 0) * a.q_sh + 8 * hi;
+    auto load_q = [&]() __attribute__((always_inline)) {
+      if (s_owner) {  // only the S waves use Q
+        // heads past num_heads (a partial last block) run on head 0's row:
+        // their scores stay finite and their output rows are never stored
+        const short* qrow = reinterpret_cast<const short*>(a.q) + (int64_t)b * a.q_sb +
+                            (int64_t)(head_ok ? head : 0) * a.q_sh + 8 * hi;
 #pragma unroll
-      for (int kc = 0; kc < NKC; ++kc) qop[kc] = *reinterpret_cast<const i16x8*>(qrow + 16 * kc);
-    }
-    if (PAGED && PAGE_UNIFORM) {
+        for (int kc = 0; kc < NKC; ++kc) qop[kc] = *reinterpret_cast<const i16x8*>(qrow + 16 * kc);
+      }
+      asm volatile("" ::: "memory");  // the copies below are issued after Q
+    };
+    auto pages_ready = [&]() __attribute__((always_inline)) {
+      if (PAGED && PAGE_UNIFORM) {
 #pragma unroll
-      for (int i = 0; i < kStages; ++i) pro_page[i] = page_ready(pro_page[i]);
+        for (int i = 0; i < kStages; ++i) pro_page[i] = page_ready(pro_page[i]);
+      }
+    };
+    if (TMLA_STARTUP == 0) {
+      load_q();
+      pages_ready();
+      issue(st0, pro_page[0]);  // nst >= 1
+      wait_vmcnt<0>();  // Q and sub-tile 0; the loop then uses Q with no further wait
+      if (nst > 1) issue(st0 + 1, pro_page[1]);
+    } else {
+      // sub-tile 1 is in flight while Q and sub-tile 0 land (mode 1: Q
+      // requested first; mode 2: sub-tile 0 first)
+      if (TMLA_STARTUP == 1) load_q();
+      pages_ready();
+      issue(st0, pro_page[0]);  // nst >= 1
+      if (TMLA_STARTUP == 2) load_q();
+      if (nst > 1) {
+        issue(st0 + 1, pro_page[1]);
+        wait_vmcnt<LOADS>();  // all but sub-tile 1's copies
+      } else {
+        wait_vmcnt<0>();
+      }
     }
-    issue(st0, pro_page[0]);  // nst >= 1
-    wait_vmcnt<0>();  // Q and sub-tile 0; the loop then uses Q with no further wait
-    if (nst > 1) issue(st0 + 1, pro_page[1]);
     int next_page = pro_page[2];  // already waited for
 
     // Iteration i (-1 <= i < nst): PV(i) from ring entry i interleaved with
