@@ -709,6 +709,7 @@ void mla_partial_kernel(PartialArgs a) {
 
   // ---- work range -------------------------------------------------------
   int b_first, tile_lo, tile_hi, off_first, n_first, chunk = 0;
+  bool snapped = false;  // balanced: one piece of one sequence per worker
   if (a.num_splits > 0) {
     const int S = a.num_splits;
     const int b = worker / S, s = worker - b * S;
@@ -740,8 +741,44 @@ void mla_partial_kernel(PartialArgs a) {
     }
     const int total = __builtin_amdgcn_readlane(incl, 63);
     chunk = (total + a.num_workers - 1) / a.num_workers;
+    // Snapped ranges: when every sequence cut into pieces of at most c tiles
+    // gives no more pieces than workers, worker w takes piece w instead (the
+    // pieces of each sequence in order, piece j = tiles [j c, (j + 1) c)).
+    // The longest range is still c tiles, and no worker pays a second
+    // start-up and finalize for a range that straddles two sequences.
+    int pcs = 0, pinc = 0;
+    if (chunk > 0) {
+      pcs = (tiles_of(len0) + chunk - 1) / chunk;  // len0 = 0 for a lane without sequences
+      for (int b = lo_b + 1; b < hi_b; ++b) pcs += (tiles_of(a.seqlens[b]) + chunk - 1) / chunk;
+      pinc = pcs;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(pinc, d);
+        if (lane0 >= d) pinc += v;
+      }
+      snapped = __builtin_amdgcn_readlane(pinc, 63) <= a.num_workers;
+    }
     const int lo = worker * chunk;
-    if (lo >= total) {  // wave-uniform, and the same in every wave
+    if (snapped && worker < __builtin_amdgcn_readlane(pinc, 63)) {
+      // the one lane whose sequences hold piece `worker` finds which of them
+      int poff = pinc - pcs, off = incl - sum, fb = lo_b, flen = len0;
+      for (int b = lo_b; b < hi_b; ++b) {
+        const int len = b == lo_b ? len0 : a.seqlens[b];
+        const int nt = tiles_of(len);
+        const int np = (nt + chunk - 1) / chunk;
+        fb = b;
+        flen = len;
+        if (worker < poff + np) break;
+        poff += np;
+        off += nt;
+      }
+      const int src = __builtin_ctzll(__ballot(pcs > 0 && pinc - pcs <= worker && worker < pinc));
+      b_first = __builtin_amdgcn_readlane(fb, src);
+      off_first = __builtin_amdgcn_readlane(off, src);
+      n_first = __builtin_amdgcn_readlane(flen, src);
+      tile_lo = (worker - __builtin_amdgcn_readlane(poff, src)) * chunk;  // local to b_first
+      tile_hi = min(tile_lo + chunk, tiles_of(n_first));
+    } else if (snapped || lo >= total) {  // wave-uniform, and the same in every wave
       if (!a.fused) return;  // (the fused tail still clears empty sequences)
       b_first = off_first = n_first = tile_lo = tile_hi = 0;
     } else {
@@ -852,7 +889,10 @@ void mla_partial_kernel(PartialArgs a) {
       }
     } else {
       const int ch = fresh_s(chunk);
-      const int g1 = seg_global_off / ch, g2 = (seg_global_off + nt_b - 1) / ch;
+      // the workers of b: g1..g2 (straddling ranges) or g1 = worker - j ..
+      // g1 + pieces - 1 (snapped: this is piece j = t_start / c of b)
+      const int g1 = snapped ? worker - t_start / ch : seg_global_off / ch;
+      const int g2 = snapped ? g1 + (nt_b + ch - 1) / ch - 1 : (seg_global_off + nt_b - 1) / ch;
       seg.slot = worker + b;
       seg.direct = g1 == g2;
       if (a.fused && !seg.direct && wave == 0 && lane == 0) {
@@ -1461,11 +1501,35 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
     __syncthreads();
     before = s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3];
     total = s_red[1][0] + s_red[1][1] + s_red[1][2] + s_red[1][3];
-    if (nt_b > 0) {
+    if (nt_b > 0) {  // (then total > 0; uniform over the workgroup)
       const int chunk = (total + a.num_workers - 1) / a.num_workers;
-      const int g1 = before / chunk, g2 = (before + nt_b - 1) / chunk;
-      count = g2 - g1 + 1;
-      slot0 = g1 + b;
+      // the partial kernel's snapped ranges when the pieces fit the workers
+      int pbefore = 0, ptotal = 0;
+      for (int i = threadIdx.x; i < a.batch; i += 256) {
+        const int np = (tiles_of(a.seqlens[i]) + chunk - 1) / chunk;
+        ptotal += np;
+        if (i < b) pbefore += np;
+      }
+      for (int d = 32; d >= 1; d >>= 1) {
+        pbefore += __shfl_xor(pbefore, d);
+        ptotal += __shfl_xor(ptotal, d);
+      }
+      __syncthreads();  // every wave has read s_red
+      if (lane == 0) {
+        s_red[0][wave] = pbefore;
+        s_red[1][wave] = ptotal;
+      }
+      __syncthreads();
+      pbefore = s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3];
+      ptotal = s_red[1][0] + s_red[1][1] + s_red[1][2] + s_red[1][3];
+      if (ptotal <= a.num_workers) {
+        count = (nt_b + chunk - 1) / chunk;
+        slot0 = pbefore + b;
+      } else {
+        const int g1 = before / chunk, g2 = (before + nt_b - 1) / chunk;
+        count = g2 - g1 + 1;
+        slot0 = g1 + b;
+      }
     }
   }
   if (head >= a.num_heads || count == 1) return;  // count == 1: written by stage 1
