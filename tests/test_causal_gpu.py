@@ -103,6 +103,36 @@ def test_causal_fp16_and_noncontiguous(gpu):
     check_causal(out, lse, q, kv, seqlens, bt, dtype=torch.float16)
 
 
+@pytest.mark.parametrize("page", [None, 16, 48])
+def test_causal_dense_and_small_pages(gpu, page):
+    """Dense cache (page size 1 in the kernel) and pages that are not whole
+    32-token sub-tiles (per-row page lookups) under the causal mask."""
+    from triton_mla import mla_decode
+
+    T, H = 3, 32
+    seqlens = torch.tensor([2, 40, 97, 530], dtype=torch.int32)
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(len(seqlens), T, H, D_LATENT + D_ROPE, generator=g).to(torch.bfloat16)
+    dense = torch.randn(len(seqlens), int(seqlens.max()), D_LATENT + D_ROPE, generator=g).to(torch.bfloat16)
+    if page is None:
+        kv, bt = dense, None
+    else:
+        per_seq = -(-dense.shape[1] // page)
+        bt = torch.randperm(len(seqlens) * per_seq, generator=g).view(len(seqlens), per_seq).int()
+        padded = torch.zeros(len(seqlens), per_seq * page, dense.shape[2], dtype=dense.dtype)
+        padded[:, : dense.shape[1]] = dense
+        kv = torch.empty(len(seqlens) * per_seq, page, dense.shape[2], dtype=dense.dtype)
+        kv[bt.long()] = padded.view(len(seqlens), per_seq, page, dense.shape[2])
+    out, lse = mla_decode(q.to(gpu), kv.to(gpu), seqlens.to(gpu), None if bt is None else bt.to(gpu),
+                          softmax_scale=SCALE, return_lse=True)
+    torch.cuda.synchronize()
+    # the oracle reads the same logical cache through a 1-row-per-page table
+    rows = dense.shape[1]
+    flat = dense.reshape(len(seqlens) * rows, 1, dense.shape[2])
+    ident = torch.arange(len(seqlens) * rows, dtype=torch.int32).view(len(seqlens), rows)
+    check_causal(out, lse, q, flat, seqlens, ident)
+
+
 def test_causal_workspace_and_errors():
     """Host-side argument handling of the causal entry point (no launch)."""
     import triton_mla._native as native
