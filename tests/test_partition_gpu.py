@@ -70,3 +70,27 @@ def test_balanced_partition_forms(gpu, seqlens, workers, snapped, heads):
     torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref_out), **OUT_TOL)
     torch.testing.assert_close(lse.cpu()[valid], torch.from_numpy(ref_lse)[valid], **LSE_TOL)
     assert torch.all(out.cpu()[~valid] == 0) and torch.all(torch.isneginf(lse.cpu()[~valid]))
+
+
+@pytest.mark.parametrize("batch", [1, 8, 40])
+def test_head_blocks_for_small_batches(gpu, batch):
+    """128 heads in workgroups of 32, 64 or 128 heads: the host picks fewer
+    heads per workgroup when the tile bound of the call (block-table width
+    times page size) leaves compute units idle (here B = 1 -> 32, B = 8 -> 64,
+    B = 40 -> 128). Every form must agree with the oracle."""
+    from triton_mla import mla_decode
+
+    g = torch.Generator().manual_seed(batch)
+    lens = torch.randint(1, 1025, (batch,), generator=g, dtype=torch.int32)
+    lens[0] = 1024
+    q = torch.randn(batch, 128, D_LATENT + D_ROPE, generator=g).to(torch.bfloat16)
+    kv = torch.randn(batch * 16, TILE, D_LATENT + D_ROPE, generator=g).to(torch.bfloat16)
+    bt = torch.randperm(batch * 16, generator=g).view(batch, 16).int()
+    out, lse = mla_decode(q.to(gpu), kv.to(gpu), lens.to(gpu), bt.to(gpu), softmax_scale=SCALE, return_lse=True)
+    out1, lse1 = mla_decode(q.to(gpu), kv.to(gpu), lens.to(gpu), bt.to(gpu), softmax_scale=SCALE, return_lse=True,
+                            single_launch=True)
+    torch.cuda.synchronize()
+    ref_out, ref_lse = oracle.mla_decode_ref(bits(q), bits(kv), lens.numpy(), bt.numpy(), D_LATENT, SCALE)
+    for o, l in ((out, lse), (out1, lse1)):
+        torch.testing.assert_close(o.float().cpu(), torch.from_numpy(ref_out), **OUT_TOL)
+        torch.testing.assert_close(l.cpu(), torch.from_numpy(ref_lse), **LSE_TOL)

@@ -1409,7 +1409,8 @@ void mla_partial_kernel(PartialArgs a) {
           dst = a.mid_o + ((int64_t)seg.slot * a.num_heads + head_base) * DV;
           row_stride = DV;
         }
-        const int rows = min(32, a.num_heads - head_base);  // wave-uniform
+        // wave-uniform; only the waves that own a head block hold staged rows
+        const int rows = wave < NHB ? min(32, a.num_heads - head_base) : 0;
         const char LDS_AS* obuf = lds + wave * 32 * OPITCH;
         // eight rows per batch: their reads are all issued before the first
         // store waits for its data
@@ -1735,10 +1736,23 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   a.spin_limit = g_spin_limit;
 
   // blocks of 32 heads per workgroup (4 waves in every case)
-  const int nhb = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
-  const int heads_per_wg = 32 * nhb;
+  int nhb = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
   const int workers = num_splits > 0 ? batch * num_splits : num_workers;
-  dim3 grid(workers, (num_heads + heads_per_wg - 1) / heads_per_wg);
+  // Upper bound of the 64-token tiles the call can hold (block-table width or
+  // dense capacity): balanced workers past it never get a range, so the grid
+  // stops there, and when the busy workgroups would leave compute units idle,
+  // fewer heads per workgroup (more, shorter workgroups: less Q to load, less
+  // MFMA work per sub-tile, smaller partial rows) use them. The single-launch
+  // merge keeps the head blocks its counters are laid out for.
+  const int64_t cap_tokens = paged ? (int64_t)bt_cols * page_size : num_blocks;
+  const int64_t tile_bound = (int64_t)batch * ((cap_tokens + kTileTokens - 1) / kTileTokens);
+  const int grid_x = num_splits > 0 ? workers : (int)(tile_bound < workers ? (tile_bound > 0 ? tile_bound : 1) : workers);
+  if (mode != 1) {
+    const int64_t cus = current_cu_count();
+    while (nhb > 1 && (int64_t)grid_x * ((num_heads + 16 * nhb - 1) / (16 * nhb)) <= cus) nhb /= 2;
+  }
+  const int heads_per_wg = 32 * nhb;
+  dim3 grid(grid_x, (num_heads + heads_per_wg - 1) / heads_per_wg);
   // The fused merge: one workgroup per compute unit at most (the kernel's LDS
   // use admits one), so that siblings normally run side by side.
   const size_t mid_o_bytes = wl.l - wl.o;  // partial rows, 256-byte aligned
