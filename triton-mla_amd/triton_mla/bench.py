@@ -84,8 +84,9 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
     nbytes = inp.algorithmic_bytes()
     flops = inp.flops()
     workers = call.workers or call.splits * inp.batch
-    config = f"hip/w{min(4, max(1, -(-inp.heads // 32)))}/" + (
-        f"balanced{workers}" if splits is None else f"splits{splits}")
+    # (the heads per workgroup are chosen inside the library from the call's
+    # shape, so the label names the partition only)
+    config = "hip/" + (f"balanced{workers}" if splits is None else f"splits{splits}")
     seqlen = int(inp.seqlens.max())
     row = [inp.batch, seqlen, args.splits, config, f"{t_hip:.1f}", f"{nbytes / t_hip / 1e6:.2f}",
            f"{flops / t_hip / 1e6:.0f}"]
