@@ -63,6 +63,10 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 #ifndef TMLA_STARTUP
 #define TMLA_STARTUP 1
 #endif
+// L2 domains the workers of one sequence are grouped by (1: no grouping)
+#ifndef TMLA_XCDS
+#define TMLA_XCDS 8
+#endif
 // 1: one LDS wait per two MFMA steps (for the operands of both)
 #ifndef TMLA_WAIT_PAIR
 #define TMLA_WAIT_PAIR 1
@@ -1721,7 +1725,7 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   if (a.qk_scale_log2 == 0.0f) a.qk_scale_log2 = 1.17549435e-38f;
   a.num_splits = num_splits;
   a.num_workers = num_workers;
-  a.xcds = 8;  // MI355X: 8 XCDs
+  a.xcds = TMLA_XCDS;  // MI355X: 8 XCDs
   a.out = static_cast<char*>(out);
   a.out_sb = out_stride_b;
   a.out_sh = out_stride_h;
