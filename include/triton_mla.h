@@ -80,7 +80,10 @@ size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v
  *              (out_stride_b, out_stride_h, 1); written for sequences that one
  *              worker completes. lse [batch, num_heads] float32 natural log.
  * Page ids are clamped to [0, num_blocks) and page slots to [0, bt_cols) so a
- * malformed table cannot address memory outside the cache.
+ * malformed table cannot address memory outside the cache. seqlens[b] must
+ * not exceed the table's capacity bt_cols * page_size (dense: num_blocks), as
+ * in the reference; the launch is sized from that capacity, so larger lengths
+ * give undefined results (still without out-of-bounds accesses).
  */
 int tmla_mla_decode_partial(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                             const void* kv, int64_t kv_stride_0, int64_t kv_stride_1,
