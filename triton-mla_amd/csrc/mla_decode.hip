@@ -63,10 +63,6 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 #ifndef TMLA_STARTUP
 #define TMLA_STARTUP 1
 #endif
-// 1: partial rows of the two-kernel form stored with plain (write-back) stores
-#ifndef TMLA_PLAIN_STORES
-#define TMLA_PLAIN_STORES 0
-#endif
 // L2 domains the workers of one sequence are grouped by (1: no grouping)
 #ifndef TMLA_XCDS
 #define TMLA_XCDS 8
@@ -1429,23 +1425,13 @@ void mla_partial_kernel(PartialArgs a) {
           for (int k = 0; k < 8; ++k) row[k] = *reinterpret_cast<const i16x8 LDS_AS*>(obuf + (r0 + k) * OPITCH + lane * 16);
 #pragma unroll
           for (int k = 0; k < 8; ++k)
-            if (r0 + k < rows) {
-              i16x8* p = reinterpret_cast<i16x8*>(dst + (r0 + k) * row_stride + lane * 8);
-              // the merge inside this launch reads the partials from other
-              // workgroups: written through; the next kernel needs no such care
-              if (!TMLA_PLAIN_STORES || a.fused)
-                store_through(p, row[k]);
-              else
-                *p = row[k];
-            }
+            if (r0 + k < rows) store_through(reinterpret_cast<i16x8*>(dst + (r0 + k) * row_stride + lane * 8), row[k]);
         }
         if (head_ok && hi == 0) {
           if (seg.direct)
             a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
-          else if (!TMLA_PLAIN_STORES || a.fused)
-            store_through_f32(a.mid_lse + (int64_t)seg.slot * a.num_heads + head, lse2);
           else
-            a.mid_lse[(int64_t)seg.slot * a.num_heads + head] = lse2;
+            store_through_f32(a.mid_lse + (int64_t)seg.slot * a.num_heads + head, lse2);
         }
         // the next segment refills the rings
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
