@@ -67,6 +67,10 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 #ifndef TMLA_XCDS
 #define TMLA_XCDS 8
 #endif
+// 1: Q staged through LDS in the KV layout before the first KV copies
+#ifndef TMLA_Q_LDS
+#define TMLA_Q_LDS 1
+#endif
 // 1: one LDS wait per two MFMA steps (for the operands of both)
 #ifndef TMLA_WAIT_PAIR
 #define TMLA_WAIT_PAIR 1
@@ -1167,7 +1171,48 @@ void mla_partial_kernel(PartialArgs a) {
         for (int i = 0; i < kStages; ++i) pro_page[i] = page_ready(pro_page[i]);
       }
     };
-    if (TMLA_STARTUP == 0) {
+    if (TMLA_Q_LDS) {
+      // Q through LDS: wave w copies its 32 rows (contiguous 1 KiB pieces,
+      // the KV copies' swizzled layout) into V ring entry w and rope entry w
+      // (wave 3: P buffer 0, written again only after the first barrier of
+      // the loop), reads Q^T back with the K-operand offsets, and only then
+      // are the rings handed to the KV copies.
+      const int qrope = s_owner ? (wave < kRopeStages ? OFF_R + wave * RSLOT : OFF_P) : 0;
+      if (s_owner) {
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int hq = head_base + 8 * rg + dma_r;
+          const char* src = a.q + ((int64_t)b * a.q_sb + (int64_t)(hq < a.num_heads ? hq : 0) * a.q_sh) * 2 +
+                            ((lane & 7) ^ piece_swizzle(dma_r, rg)) * 16;
+          static_for<NCB>([&](auto CB) __attribute__((always_inline)) {
+            constexpr int cb = decltype(CB)::value;
+            char LDS_AS* dst = cb < NVB ? lds + wave * VSLOT + (rg * NVB + cb) * 1024
+                                        : lds + qrope + (rg * NRB + cb - NVB) * 1024;
+            lds_copy16<cb * 128>(src, dst);
+          });
+        }
+      }
+      wait_vmcnt<0>();
+      if (s_owner) {
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) {
+          const int cb = kc >> 2;
+          const char LDS_AS* p = cb < NVB ? lds + wave * VSLOT + k_off_v[kc & 3] + cb * 1024
+                                          : lds + qrope - OFF_R + k_off_r[kc & 3] + (cb - NVB) * 1024;
+          qop[kc] = *reinterpret_cast<const i16x8 LDS_AS*>(p);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      lds_barrier();  // every wave has its Q^T before the rings are refilled
+      pages_ready();
+      issue(st0, pro_page[0]);  // nst >= 1
+      if (nst > 1) {
+        issue(st0 + 1, pro_page[1]);
+        wait_vmcnt<LOADS>();
+      } else {
+        wait_vmcnt<0>();
+      }
+    } else if (TMLA_STARTUP == 0) {
       load_q();
       pages_ready();
       issue(st0, pro_page[0]);  // nst >= 1
