@@ -2,22 +2,34 @@
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 10]
 
-A step is one mla_decode (split-KV partial kernel + log-sum-exp combine) over
-the measured workload: batch 32, 128 heads, 8192 cached tokens per sequence,
-bf16, page size 64, shuffled block tables, inputs ~ N(0, 1) drawn on the CPU
-with seed 0 and resident in HBM before timing. Every step is preceded by a
-512 MiB read that evicts the 256 MiB Infinity Cache (a read, so no dirty
-lines are left for the timed kernels to write back); HIP events on the
-launch stream bracket each kernel.
+A step is one mla_decode over the measured workload: batch 32, 128 heads,
+8192 cached tokens per sequence, bf16, page size 64, shuffled block tables,
+inputs ~ N(0, 1) drawn on the CPU with seed 0 and resident in HBM before
+timing. Every launch is preceded by a 512 MiB read that evicts the 256 MiB
+Infinity Cache (a read, so no dirty lines are left for the timed kernels to
+write back); HIP events on the launch stream bracket each launch.
+
+The timed region runs the K steps three ways, interleaved step by step so
+that no form is always the one measured first after the warm-up:
+  * the two-kernel form (tmla_mla_decode: partial + combine kernels),
+  * the single launch (tmla_mla_decode_fused: the merge inside the partial
+    kernel),
+  * the partial kernel alone (the dominant kernel of the roofline).
+``value`` is the form mla_decode() runs by default; the other is reported
+beside it with min / median / p90. After the timed region, the public
+``triton_mla.mla_decode(...)`` call (output and workspace allocation and the
+host-side argument checks included) is timed the way the reference's bench
+times it.
 
 ``--copy-mib N`` adds, after the timed steps, three device-to-device copies
 of N MiB: kernels of known traffic against which the HBM counters of a
 profiler run (FETCH_SIZE, WRITE_SIZE) are scaled.
 
 Prints one JSON line: throughput in TFLOP/s (flops = 2 * H * (576 + 512) per
-cached token), microseconds per step, the HBM roofline of the dominant
-(partial) kernel and the CPU oracle timed on a bounded sample of the same
-workload on this host's cores.
+cached token), microseconds per step, the HBM roofline of the partial kernel
+and the reference's CPU path (float32 torch ``mla_decode_ref``, per
+sequence, and the eager batched ``mla_decode_torch``) timed on this host's
+cores; the float64 C oracle is the correctness gate.
 """
 
 from __future__ import annotations
@@ -42,10 +54,10 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
-    p.add_argument("--warmup", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--splits", default="balanced",
                    help="'balanced' (device-side tile balancing) or an integer split count")
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-oracle sample time")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on each CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-flush", action="store_true", help="do not evict caches between steps")
     p.add_argument("--copy-mib", type=int, default=0,
@@ -53,45 +65,58 @@ def parse():
     return p.parse_args()
 
 
+def spread(times):
+    t = sorted(times)
+    return {"min": round(t[0], 2), "median": round(statistics.median(t), 2),
+            "p90": round(t[min(len(t) - 1, int(0.9 * len(t)))], 2), "mean": round(statistics.fmean(t), 2)}
+
+
 def cpu_baseline(inp, target_s):
-    """Time the float64 CPU oracle (oracle/mla_oracle.c) on the first n sequences."""
-    import numpy as np
+    """The reference's CPU path on this host's cores: the float32 per-sequence
+    mla_decode_ref (src/triton_mla/reference.py:16-31) on the whole workload
+    (median of 3 after a warm-up run, each bounded by target_s), and the
+    eager batched mla_decode_torch (reference.py:34-44) on the sequences that
+    fit target_s."""
     import torch
 
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle
+    from triton_mla.reference import mla_decode_ref, mla_decode_torch
 
-    threads = len(os.sched_getaffinity(0))
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    args = (inp.q, inp.kv_cache, inp.seqlens, inp.block_table, 512, inp.softmax_scale)
 
-    def u16(t):
-        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
-
-    q, kv, lens, bt = u16(inp.q), u16(inp.kv_cache), inp.seqlens.numpy(), inp.block_table.numpy()
-
-    def run(n):
+    def timed(fn, n):
         t0 = time.perf_counter()
-        out, lse = oracle.mla_decode_ref(q[:n], kv, lens[:n], bt[:n], 512, inp.softmax_scale,
-                                         nthreads=threads)
-        return time.perf_counter() - t0, out, lse
+        fn(inp.q[:n], inp.kv_cache, inp.seqlens[:n], inp.block_table[:n], 512, inp.softmax_scale)
+        return time.perf_counter() - t0
 
-    t1, _, _ = run(1)
-    n = int(max(1, min(inp.batch, round(target_s / max(t1, 1e-3)))))
-    t, out, lse = run(n)
-    flops = int(lens[:n].sum()) * inp.heads * 2 * (576 + 512)
-    return {"seconds": t, "sequences": n, "flops": flops, "threads": threads, "out": out, "lse": lse}
+    # fp32 reference: whole workload if a first sequence says it fits
+    t1 = timed(mla_decode_ref, 1)
+    n_ref = int(max(1, min(inp.batch, target_s / max(t1, 1e-4))))
+    runs = [timed(mla_decode_ref, n_ref) for _ in range(3)]
+    t_ref = statistics.median(runs)
+    out_ref, _ = mla_decode_ref(*args) if n_ref == inp.batch else (None, None)
+    # eager batched torch path (bf16 matmuls on the CPU)
+    t1 = timed(mla_decode_torch, 1)
+    n_torch = int(max(1, min(inp.batch, target_s / max(t1, 1e-4))))
+    t_torch = timed(mla_decode_torch, n_torch)
+    return {"cores": cores, "n_ref": n_ref, "t_ref": t_ref, "n_torch": n_torch, "t_torch": t_torch,
+            "out_ref": out_ref}
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
-              "(the decode path runs and is measured on a single MI355X)", file=sys.stderr)
+              "(the decode path runs and is measured on a single MI355X; see DESIGN.md for how "
+              "it would shard)", file=sys.stderr)
         sys.exit(2)
 
     import torch
 
+    import triton_mla
     from triton_mla import workloads
-    from triton_mla.kernel import DecodeLaunch
+    from triton_mla.kernel import DecodeLaunch, DEFAULT_SINGLE_LAUNCH
     from triton_mla.timing import Flusher
 
     dev = torch.device("cuda:0")
@@ -101,66 +126,85 @@ def main():
     call = DecodeLaunch(inp.q, inp.kv_cache, inp.seqlens, inp.block_table, 512, inp.softmax_scale, splits)
     flush = None if args.no_flush else Flusher(dev)
     stream = torch.cuda.current_stream(dev)
+    default_single = DEFAULT_SINGLE_LAUNCH and call.fused
 
+    forms = {
+        "two_kernel": lambda: call.run(single_launch=False),
+        "single_launch": lambda: call.run(single_launch=True),
+        "partial_only": call.partial,
+    }
+    if not call.fused:
+        del forms["single_launch"]
     for _ in range(args.warmup):
-        if flush:
-            flush()
-        call.run()
+        for fn in forms.values():
+            if flush:
+                flush()
+            fn()
     torch.cuda.synchronize(dev)
 
-    # timed region: each step is one mla_decode (tmla_mla_decode: partial +
-    # combine, no event between the kernels) between two events on the launch
-    # stream
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    # timed region: K steps of each form, interleaved step by step
+    ev = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)] for k in forms}
     torch.cuda.synchronize(dev)
     wall0 = time.perf_counter()
     for i in range(args.steps):
-        if flush:
-            flush()
-        ev[i][0].record(stream)
-        call.run()
-        ev[i][1].record(stream)
+        for k, fn in forms.items():
+            if flush:
+                flush()
+            ev[k][i][0].record(stream)
+            fn()
+            ev[k][i][1].record(stream)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - wall0
+    us = {k: [a.elapsed_time(b) * 1e3 for a, b in v] for k, v in ev.items()}
 
-    # the dominant kernel alone, same number of launches, for the roofline
-    evp = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
-    for i in range(args.steps):
-        if flush:
-            flush()
-        evp[i][0].record(stream)
-        call.partial()
-        evp[i][1].record(stream)
+    headline = "single_launch" if default_single else "two_kernel"
+    # outputs of both forms on the same inputs: the same merge code on the same partials
+    call.run(single_launch=False)
     torch.cuda.synchronize(dev)
-
-    # the single-launch form (tmla_mla_decode_fused, merge inside the partial
-    # kernel) on the same inputs, for comparison
-    ev1 = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
-    for i in range(args.steps):
-        if flush:
-            flush()
-        ev1[i][0].record(stream)
+    eager_out = call.out.clone()
+    single_same = None
+    if call.fused:
+        call.out.fill_(1.0)
         call.run(single_launch=True)
-        ev1[i][1].record(stream)
+        torch.cuda.synchronize(dev)
+        single_same = torch.equal(call.out, eager_out)
+
+    # the public call, as the reference's bench times it (bench.py:68-69, 78):
+    # fresh outputs and workspace, host-side checks and launches per call
+    pub_fn = lambda: triton_mla.mla_decode(inp.q, inp.kv_cache, inp.seqlens, inp.block_table,  # noqa: E731
+                                           softmax_scale=inp.softmax_scale, num_splits=splits)
+    for _ in range(3):
+        pub_fn()
     torch.cuda.synchronize(dev)
-    single_out = call.out.clone()
+    evq = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    host_us = []
+    for i in range(args.steps):
+        if flush:
+            flush()
+        evq[i][0].record(stream)
+        t0 = time.perf_counter()
+        pub_out = pub_fn()
+        host_us.append((time.perf_counter() - t0) * 1e6)
+        evq[i][1].record(stream)
+    torch.cuda.synchronize(dev)
+    public_us = [a.elapsed_time(b) * 1e3 for a, b in evq]
+    public_same = torch.equal(pub_out, eager_out)
 
     # the same step captured once in a HIP graph and replayed (how a serving
     # loop launches it): every replay must reproduce the eager result exactly
-    call.run()
-    torch.cuda.synchronize(dev)
-    eager_out = call.out.clone()
     graph_ok = None
     try:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            call.run()
+            forms[headline]()
         graph_ok = True
         for _ in range(3):
             call.out.zero_()
             graph.replay()
             torch.cuda.synchronize(dev)
             graph_ok = graph_ok and torch.equal(call.out, eager_out)
+            torch.randn(1024, device=dev).sum().item()  # eager work between replays
         del graph
     except RuntimeError as exc:  # capture unsupported in this environment
         print(f"graph capture failed: {exc}", file=sys.stderr)
@@ -175,17 +219,12 @@ def main():
         torch.cuda.synchronize(dev)
         del src, dst
 
-    step_us = [e[0].elapsed_time(e[1]) * 1e3 for e in ev]
-    partial_us = [e[0].elapsed_time(e[1]) * 1e3 for e in evp]
-    single_us = statistics.median([e[0].elapsed_time(e[1]) * 1e3 for e in ev1])
-    # the fused merge and stage 2 run the same merge code on the same partials
-    single_same = torch.equal(single_out, eager_out)
-    us = statistics.median(step_us)
-    p_us = statistics.fmean(partial_us)
-
+    step = us[headline]
+    t_med = statistics.median(step)
+    p_us = statistics.fmean(us["partial_only"])
     nbytes = inp.algorithmic_bytes()
     flops = inp.flops()
-    tflops = flops / (us * 1e-6) / 1e12
+    tflops = flops / (t_med * 1e-6) / 1e12
     achieved_gbs = nbytes / (p_us * 1e-6) / 1e9
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
@@ -198,43 +237,67 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(us / 1e3, 5),
-        "us_per_step": round(us, 2),
+        "ms_per_step": round(t_med / 1e3, 5),
+        "us_per_step": round(t_med, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (randn q/cache, randperm block tables, seed 0)",
         "config": {"workload": inp.name, "batch": inp.batch, "heads": inp.heads, "seq_len": 8192,
-                   "page_size": 64, "num_splits": args.splits, "cache_flush_mib": 0 if args.no_flush else 512},
+                   "page_size": 64, "num_splits": args.splits, "cache_flush_mib": 0 if args.no_flush else 512,
+                   "form": headline},
         "roofline": {"bound": "hbm", "kernel": "mla_partial_kernel", "achieved": round(achieved_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "algorithmic_bytes": nbytes,
-                     "partial_us_mean": round(p_us, 2), "step_us_mean": round(statistics.fmean(step_us), 2),
-                     "step_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "partial_us_mean": round(p_us, 2),
+                     "step_frac": round(nbytes / (t_med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
-        "single_launch_us_per_step": round(single_us, 2) if call.fused else None,
+        "step_us": {k: spread(v) for k, v in us.items()},
         "single_launch_matches": single_same,
+        "public_call_us": spread(public_us),
+        "public_call_host_us": spread(host_us),
+        "public_call_matches": public_same,
         "wall_s_timed_region": round(wall, 4),
+        "timed_launches": {k: args.steps for k in us},
         "graph_replay_matches_eager": graph_ok,
     }
 
     if not args.no_cpu_baseline:
-        cb = cpu_baseline(workloads.b32_h128_8k(), args.cpu_seconds)
-        n = cb["sequences"]
-        out_gpu = call.out[:n].float().cpu()
-        err = (out_gpu - torch.from_numpy(cb["out"])).abs().max().item()
+        import numpy as np
+
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+
+        host = workloads.b32_h128_8k()
+        # correctness gate: the float64 C oracle on the first two sequences
+        n = 2
+
+        def u16(t):
+            return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+        ref_out, _ = oracle.mla_decode_ref(u16(host.q[:n]), u16(host.kv_cache), host.seqlens[:n].numpy(),
+                                           host.block_table[:n].numpy(), 512, host.softmax_scale)
+        err = (eager_out[:n].float().cpu() - torch.from_numpy(ref_out)).abs().max().item()
         if not err <= 1e-2:
             print(f"correctness gate failed: max |gpu - oracle| = {err}", file=sys.stderr)
             sys.exit(1)
-        cpu_tflops = cb["flops"] / cb["seconds"] / 1e12
+        cb = cpu_baseline(host, args.cpu_seconds)
+        per_seq_flops = flops / inp.batch
+        cpu_tflops = cb["n_ref"] * per_seq_flops / cb["t_ref"] / 1e12
         result["cpu_baseline"] = {
-            "value": round(cpu_tflops, 5), "unit": "TFLOP/s", "cores": cb["threads"], "kind": "port",
-            "sample": f"float64 C oracle (oracle/mla_oracle.c) on the first {n} of 32 sequences "
-                      f"(8192 tokens, 128 heads each): {cb['seconds']:.2f} s",
-            "us_per_step_equiv": round(cb["seconds"] / n * inp.batch * 1e6, 1),
+            "value": round(cpu_tflops, 5), "unit": "TFLOP/s", "cores": cb["cores"], "kind": "port",
+            "sample": f"float32 torch mla_decode_ref (reference.py:16-31, per sequence) on {cb['n_ref']} of "
+                      f"{inp.batch} sequences (8192 tokens, 128 heads), median of 3: {cb['t_ref']:.3f} s",
+            "us_per_step_equiv": round(cb["t_ref"] / cb["n_ref"] * inp.batch * 1e6, 1),
+            "eager_torch": {"value": round(cb["n_torch"] * per_seq_flops / cb["t_torch"] / 1e12, 5),
+                            "unit": "TFLOP/s", "sample": f"mla_decode_torch (reference.py:34-44) on "
+                            f"{cb['n_torch']} sequences: {cb['t_torch']:.3f} s"},
             "gpu_vs_oracle_max_abs_err": err,
         }
+        if cb["out_ref"] is not None:
+            result["cpu_baseline"]["gpu_vs_cpu_ref_max_abs_err"] = \
+                (eager_out.float().cpu() - cb["out_ref"].float()).abs().max().item()
     print(json.dumps(result), flush=True)
 
 

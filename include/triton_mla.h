@@ -51,16 +51,30 @@ const char* tmla_last_error(void);
 int tmla_version(void);
 
 /*
- * Bytes of device workspace tmla_mla_decode / _partial / _combine need:
- * partial outputs (input dtype [slots, H, head_dim_v]), base-2 log-sum-exps
- * (float32 [slots, H]) and the int32 counters of the fused merge;
+ * Bytes of device workspace tmla_mla_decode / _partial / _combine / _fused
+ * need: partial outputs (input dtype [slots, H, head_dim_v]) and their
+ * base-2 log-sum-exps (float32 [slots, H]) from the start of the buffer, and
+ * the int32 counters of the single launch's merge in a block at the END of
+ * the buffer (its size rounded down to 256 bytes);
  * slots = batch * num_splits (uniform) or num_workers + batch (balanced).
- * Zero-fill the workspace once before its first use by tmla_mla_decode;
- * every call leaves the counters at zero again (a workspace may be reused
- * by any later call with the same or smaller arguments, one call at a time).
+ * The two-kernel entry points need no initialisation. A workspace may be
+ * reused by any later call whose tmla_workspace_bytes is no larger, one
+ * call at a time.
  */
 size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v,
                             int32_t num_splits, int32_t num_workers);
+
+/*
+ * Bytes at the end of the workspace that must be zero before its first use
+ * by tmla_mla_decode_fused (or tmla_mla_decode_causal with single_launch):
+ * zero the last min(tmla_workspace_zero_bytes(...), workspace_bytes) bytes
+ * once, with the arguments of the largest call the buffer will serve. Every
+ * single launch leaves its counters at zero again, and the partials of no
+ * call reach that suffix, so later calls of any size up to it need nothing.
+ * No counterpart in the reference (its two launches need no counters).
+ */
+size_t tmla_workspace_zero_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v,
+                                 int32_t num_splits, int32_t num_workers);
 
 /*
  * Stage 1: split-KV partial attention.
@@ -126,15 +140,15 @@ int tmla_mla_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
  * The same call as ONE launch (no counterpart in the reference, which always
  * launches two kernels): when every workgroup of stage 1 fits on the device
  * at once (workers times head blocks of up to 128 heads at most the CU
- * count), the workers of a split sequence merge its partials themselves,
- * each a share of the heads, once all of them have stored theirs (a bounded
- * wait: a worker that stops waiting hands its share to the one whose arrival
- * completes the count). Otherwise it runs both stages like tmla_mla_decode.
- * Results equal tmla_mla_decode's bit for bit. The workspace must be
- * zero-filled before its first use (tmla_workspace_bytes). On MI355X the
- * two-kernel form is as fast or faster for the measured shapes (the merge
- * reads back every partial either way); this form is for callers that need
- * a single launch.
+ * count; tmla_mla_decode_fused_is_single tells), the workers of a split
+ * sequence merge its partials themselves, each a share of the heads, once
+ * all of them have stored theirs (a bounded wait of spin_limit polls, about
+ * 2^7 clocks apart; < 0 selects the default, 16384; 0 makes every worker
+ * that does not complete the count hand its share over at once). A worker
+ * that stops waiting hands its share to the one whose arrival completes the
+ * count. Otherwise it runs both stages like tmla_mla_decode. Results equal
+ * tmla_mla_decode's bit for bit. The workspace's counter suffix must be
+ * zero before its first use (tmla_workspace_zero_bytes).
  */
 int tmla_mla_decode_fused(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
                           int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks,
@@ -143,7 +157,17 @@ int tmla_mla_decode_fused(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale,
                           int32_t num_splits, int32_t num_workers, void* out, int64_t out_stride_b,
                           int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes,
-                          void* stream);
+                          int32_t spin_limit, void* stream);
+
+/*
+ * 1 when tmla_mla_decode_fused with these arguments runs as a single launch
+ * on `device`, 0 when it runs both stages. capacity_tokens = bt_cols *
+ * page_size for a paged cache, the dense capacity otherwise (the launch
+ * trims its grid to the tiles that capacity allows).
+ */
+int32_t tmla_mla_decode_fused_is_single(int32_t batch, int32_t num_heads, int32_t head_dim_v,
+                                        int32_t num_splits, int32_t num_workers,
+                                        int64_t capacity_tokens, int32_t device);
 
 /*
  * Multi-token (causal) decode, no counterpart in the reference (its
@@ -160,8 +184,8 @@ int tmla_mla_decode_fused(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  *   out  [batch, q_len * num_heads, head_dim_v] the same way; lse [batch,
  *        q_len * num_heads] float32 natural log.
  * The workspace is tmla_workspace_bytes(batch, q_len * num_heads, ...).
- * single_launch != 0 runs like tmla_mla_decode_fused, else like
- * tmla_mla_decode. q_len = 1 gives tmla_mla_decode's results bit for bit.
+ * single_launch != 0 runs like tmla_mla_decode_fused (default spin limit),
+ * else like tmla_mla_decode. q_len = 1 gives tmla_mla_decode's results bit for bit.
  */
 int tmla_mla_decode_causal(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
                            int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks,
@@ -173,15 +197,6 @@ int tmla_mla_decode_causal(const void* q, int64_t q_stride_b, int64_t q_stride_h
                            size_t workspace_bytes, int32_t single_launch, void* stream);
 /* Number of compute units of `device` (0 on error); the default worker count. */
 int32_t tmla_device_cu_count(int32_t device);
-
-/*
- * Test hook, no counterpart in the reference: the number of polls (about
- * 2^7 clocks apart) a worker of the fused merge waits for its siblings
- * before it hands its share over; polls < 0 only queries. Returns the
- * previous value (default 16384). 0 makes every share go to the worker that
- * completes the count, which tests that path.
- */
-int32_t tmla_set_merge_spin_limit(int32_t polls);
 
 /*
  * MLA layer glue: the absorbed-projection steps on either side of

@@ -116,10 +116,20 @@ def test_mla_layer_deepseek_v3_dims(gpu):
     """MLA.forward at DeepSeek-V3 dims, B=16, 16K cached tokens (seeded N(0, 0.02)
     weights, N(0, 1) cache and hidden states) against the oracle's float64
     absorbed step: projections, RoPE, RMSNorm, cache append, attention (C
-    oracle) and W_UV / wo. The GPU runs its projections in bf16, so the bound
-    is on the relative L2 error of the layer output (and of the appended cache
-    rows), chosen for a chain of bf16 GEMMs."""
-    from triton_mla import MLA, MLAConfig
+    oracle) and W_UV / wo.
+
+    Three elementwise checks:
+      * the latent decode at this shape (16 sequences x 16,385 tokens, 128
+        heads: the snapped split of 17 workers per sequence) on the oracle's
+        own query and cache: out within atol = rtol = 1e-2, lse within 1e-3;
+      * the appended cache rows: atol = rtol = 1e-2 (the GPU's projections
+        round to bf16 before the norm and the rotation);
+      * the layer output: within half a bf16 ulp plus 2^-7 * sum_i |o_i w_ji|
+        (the wo product of the oracle's W_UV output o with the weights: a
+        relative error of 2^-7 in every o_i, about four bf16 roundings of the
+        chain of bf16 GEMMs before it), and within the reference's own layer
+        tolerance atol = rtol = 3e-2 (tests/test_model.py:34-35)."""
+    from triton_mla import MLA, MLAConfig, mla_decode
 
     cfg = MLAConfig()
     batch, ctx, page = 16, 16384, 64
@@ -154,16 +164,32 @@ def test_mla_layer_deepseek_v3_dims(gpu):
     page_ids = bt.numpy()[np.arange(batch), pos // page]
     cache_bits[page_ids, pos % page] = oracle.float_to_half(entries, "bf16")
     q_abs = oracle.float_to_half(oracle.layer_absorbed_query(w, ocfg, q_nope, q_pe), "bf16")
-    o_lat, _ = oracle.mla_decode_ref(q_abs, cache_bits, pos + 1, bt.numpy(), cfg.kv_lora_rank,
-                                     (cfg.qk_head_dim) ** -0.5, dtype="bf16")
+    scale = (cfg.qk_head_dim) ** -0.5
+    o_lat, lse_lat = oracle.mla_decode_ref(q_abs, cache_bits, pos + 1, bt.numpy(), cfg.kv_lora_rank, scale,
+                                           dtype="bf16")
     ref = oracle.layer_output(w, ocfg, o_lat)
 
-    def rel(a, b):
-        return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+    # 1. the decode inside the layer, on the oracle's own query and cache
+    def from_bits(b):
+        return torch.from_numpy(b.view(np.int16)).view(torch.bfloat16)
 
+    o_gpu, lse_gpu = mla_decode(from_bits(q_abs).to(gpu), from_bits(cache_bits).to(gpu),
+                                torch.from_numpy(pos + 1).to(gpu), bt.to(gpu), head_dim_v=cfg.kv_lora_rank,
+                                softmax_scale=scale, return_lse=True)
+    torch.testing.assert_close(o_gpu.float().cpu(), torch.from_numpy(o_lat).float(), atol=1e-2, rtol=1e-2)
+    torch.testing.assert_close(lse_gpu.cpu(), torch.from_numpy(lse_lat).float(), atol=1e-3, rtol=1e-3)
+
+    # 2. the appended rows
     appended = gcache[torch.from_numpy(page_ids).long().to(gpu), torch.from_numpy(pos % page).long().to(gpu)]
-    e_rel = rel(appended.float().cpu().numpy().astype(np.float64), entries)
-    o_rel = rel(out.float().cpu().numpy().astype(np.float64), ref)
-    print(f"appended rows rel err {e_rel:.2e}, layer output rel err {o_rel:.2e}", flush=True)
-    assert e_rel < 1e-2
-    assert o_rel < 3e-2
+    torch.testing.assert_close(appended.float().cpu(), torch.from_numpy(entries).float(), atol=1e-2, rtol=1e-2)
+
+    # 3. the layer output
+    o_v = np.einsum("bhc,hdc->bhd", o_lat, w["wkv_b"].reshape(cfg.num_heads, -1, cfg.kv_lora_rank)
+                    [:, cfg.qk_nope_head_dim:]).reshape(batch, -1)
+    gemm_mag = np.abs(o_v) @ np.abs(w["wo"]).T  # sum_i |o_i w_ji|
+    got = out.float().cpu().numpy().astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -126))) - 7)
+    ratio = np.abs(got - ref) / (0.5 * ulp + 2.0 ** -7 * gemm_mag)
+    print(f"layer output: max err / bound {ratio.max():.3f}", flush=True)
+    assert ratio.max() <= 1.0
+    torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref).float(), atol=3e-2, rtol=3e-2)

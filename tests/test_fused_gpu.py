@@ -13,9 +13,10 @@ sequence; workers whose range straddles two split sequences (both of their
 merge records in use); the uniform split; empty sequences (out = 0,
 lse = -inf, cleared by the single launch itself); 16, 64, 128 and 200 heads
 (one or two head blocks per worker); fp16; repeated calls on one workspace
-(the merge counters return to zero); the hand-over path (spin limit 0: every
-worker that does not complete the count gives its share to the one that
-does); and HIP-graph replays.
+(the merge counters return to zero); one workspace shared by calls of
+different sizes; the hand-over path (spin limit 0: every worker that does not
+complete the count gives its share to the one that does); and HIP-graph
+replays.
 """
 
 import pytest
@@ -43,10 +44,10 @@ def two_stage(call):
     return call.out.clone(), call.lse.clone()
 
 
-def single(call):
+def single(call, spin_limit=-1):
     call.out.fill_(1.0)  # every element must be written by the launch
     call.lse.fill_(1.0)
-    call.run(single_launch=True)
+    call.run(single_launch=True, spin_limit=spin_limit)
     torch.cuda.synchronize()
     return call.out.clone(), call.lse.clone()
 
@@ -111,21 +112,64 @@ def test_single_launch_equals_two_kernels(gpu, name, splits, workers):
 
 @pytest.mark.parametrize("name,splits,workers", [CASES[0], CASES[2], CASES[3], CASES[5]])
 def test_hand_over_path(gpu, name, splits, workers):
-    """Spin limit 0: a worker that does not complete its sequence's count
-    hands its share over at once; the worker that completes the count merges
-    it. Same bits as the two-kernel form, and the counters still reset."""
-    from triton_mla import _native
-
-    lib = _native.load()
+    """Spin limit 0 (a per-call argument): a worker that does not complete
+    its sequence's count hands its share over at once; the worker that
+    completes the count merges it. Same bits as the two-kernel form, and the
+    counters still reset (the next call with the default limit agrees)."""
     call = launch(case(name), gpu, splits, workers)
     ref = two_stage(call)
-    prev = lib.tmla_set_merge_spin_limit(0)
-    try:
-        assert_same(single(call), ref, f"{name} hand-over")
-        assert_same(single(call), ref, f"{name} hand-over, second call")
-    finally:
-        lib.tmla_set_merge_spin_limit(prev)
+    assert_same(single(call, spin_limit=0), ref, f"{name} hand-over")
+    assert_same(single(call, spin_limit=0), ref, f"{name} hand-over, second call")
     assert_same(single(call), ref, f"{name} after hand-over")
+
+
+def fused_on(lib, call, workspace, stream):
+    """tmla_mla_decode_fused with call's arguments on another workspace."""
+    from triton_mla import _native
+
+    args = call._partial_args[:-2] + (workspace.data_ptr(), workspace.numel())
+    _native.check(lib.tmla_mla_decode_fused(*args, -1, stream), "tmla_mla_decode_fused")
+
+
+def test_workspace_reuse_across_sizes(gpu):
+    """One workspace sized for the largest call serves smaller and larger
+    calls in any order: the merge counters sit at the end of the buffer, so
+    no call's partial rows overwrite another call's counters. The buffer is
+    filled with garbage except the counter suffix (tmla_workspace_zero_bytes)."""
+    from triton_mla import _native, workloads
+
+    lib = _native.load()
+    big = launch(workloads.b32_h128_8k(), gpu)
+    small = launch(workloads.b8_h128_1k(), gpu)
+    mid = launch(case("ragged_h128"), gpu)
+    calls = {"big": big, "small": small, "mid": mid}
+    for name, c in calls.items():
+        assert c.fused, f"{name} must take the single-launch path"
+        assert c.ws_bytes <= big.ws_bytes
+    refs = {name: two_stage(c) for name, c in calls.items()}
+    ws = torch.full((big.ws_bytes,), 0x5A, dtype=torch.uint8, device=gpu)
+    z = min(lib.tmla_workspace_zero_bytes(big.batch, big.num_heads, 512, big.splits, big.workers), big.ws_bytes)
+    ws[big.ws_bytes - z:].zero_()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    for name in ["big", "small", "big", "mid", "small", "mid", "big"]:
+        c = calls[name]
+        c.out.fill_(1.0)
+        c.lse.fill_(1.0)
+        fused_on(lib, c, ws, stream)
+        torch.cuda.synchronize()
+        assert_same((c.out.clone(), c.lse.clone()), refs[name], f"{name} on the shared workspace")
+
+
+def test_fuse_decision_matches_launch(gpu):
+    """DecodeLaunch.fused comes from the library's own plan: a call it
+    reports as single-launch needs no combine kernel (stage 2 after it would
+    be redundant), and a grid larger than the device is reported as two-stage."""
+    from triton_mla import workloads
+
+    assert launch(workloads.b32_h128_8k(), gpu).fused
+    assert launch(workloads.b1_h128_1k(), gpu).fused
+    # 64 sequences x 128 heads with 512 uniform splits cannot be resident at once
+    assert not launch(workloads.uniform(64, 128, 2048), gpu, num_splits=8).fused
 
 
 def test_headline_against_oracle(gpu):

@@ -32,6 +32,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <utility>
 
 #include "cdna.h"
@@ -1618,11 +1619,18 @@ int head_blocks(int32_t heads) {
   return (heads + per - 1) / per;
 }
 
-// Workspace: partial rows [slots, H, dv] (input dtype), their base-2 lse
-// [slots, H] (float), then the fused merge's int32 counters m_count and
-// m_done [batch, head blocks] and flags m_flag [slots, head blocks].
+// Workspace of a call: partial rows [slots, H, dv] (input dtype) at offset 0,
+// their base-2 lse [slots, H] (float) after them, and the fused merge's int32
+// counters m_count and m_done [batch, head blocks] and flags m_flag [slots,
+// head blocks] in a block anchored at the END of the caller's buffer (its size
+// rounded down to 256 bytes). Anchored there, the counter block of every call
+// no larger than the one the buffer was sized for lies in the same suffix,
+// which no call's partials reach: the suffix is zero-filled once, and every
+// single launch leaves its counters at zero again.
 struct WsLayout {
-  size_t o, l, cnt, done, flag, total;  // byte offsets and size
+  size_t o, l, part_end;  // byte offsets: partial rows, lse, end of both
+  size_t cnt_bytes;       // counter block (a multiple of 256)
+  size_t total;           // part_end + cnt_bytes: the bytes the call needs
 };
 
 WsLayout ws_layout(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
@@ -1632,10 +1640,9 @@ WsLayout ws_layout(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int
   WsLayout w;
   w.o = 0;
   w.l = al((size_t)slots * heads * dv * 2);
-  w.cnt = w.l + al((size_t)slots * heads * sizeof(float));
-  w.done = w.cnt + (size_t)batch * gy * 4;
-  w.flag = w.done + (size_t)batch * gy * 4;
-  w.total = w.flag + (size_t)slots * gy * 4;
+  w.part_end = w.l + al((size_t)slots * heads * sizeof(float));
+  w.cnt_bytes = al((size_t)(2 * (int64_t)batch + slots) * gy * 4);
+  w.total = w.part_end + w.cnt_bytes;
   return w;
 }
 
@@ -1644,18 +1651,57 @@ size_t workspace_bytes(int32_t batch, int32_t heads, int32_t dv, int32_t splits,
   return ws_layout(batch, heads, dv, splits, workers).total;
 }
 
-int g_spin_limit = 1 << 14;  // polls (about 2^7 clocks each) before a share is handed over
+constexpr int kDefaultSpinLimit = 1 << 14;  // polls (about 2^7 clocks each) before a share is handed over
 
-// Compute units of the current device, cached.
+// Compute units of the current device, read once per device (relaxed atomics:
+// concurrent first calls store the same value).
 int current_cu_count() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-  if (dev < 64 && cache[dev] > 0) return cache[dev];
+  if (dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int n = 0;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (dev < 64) cache[dev] = n;
+  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
   return n;
+}
+
+// Launch shape of a decode call: blocks of 32 heads per workgroup (1, 2 or 4)
+// and the grid, and whether the single launch merges in-kernel.
+struct LaunchPlan {
+  int nhb;
+  dim3 grid;
+  bool fused;
+};
+
+// capacity_tokens: tokens the block table (or dense cache) can hold per
+// sequence; mode as in decode_launch.
+LaunchPlan plan_launch(int32_t batch, int32_t num_heads, int32_t num_splits, int32_t num_workers,
+                       int64_t capacity_tokens, size_t mid_o_bytes, int mode, int cus) {
+  LaunchPlan p;
+  p.nhb = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
+  const int workers = num_splits > 0 ? batch * num_splits : num_workers;
+  // Upper bound of the 64-token tiles the call can hold (block-table width or
+  // dense capacity): balanced workers past it never get a range, so the grid
+  // stops there, and when the busy workgroups would leave compute units idle,
+  // fewer heads per workgroup (more, shorter workgroups: less Q to load, less
+  // MFMA work per sub-tile, smaller partial rows) use them. The single-launch
+  // merge keeps the head blocks its counters are laid out for.
+  const int64_t tile_bound = (int64_t)batch * ((capacity_tokens + kTileTokens - 1) / kTileTokens);
+  const int grid_x =
+      num_splits > 0 ? workers : (int)(tile_bound < workers ? (tile_bound > 0 ? tile_bound : 1) : workers);
+  if (mode != 1) {
+    while (p.nhb > 1 && (int64_t)grid_x * ((num_heads + 16 * p.nhb - 1) / (16 * p.nhb)) <= cus) p.nhb /= 2;
+  }
+  const int heads_per_wg = 32 * p.nhb;
+  p.grid = dim3(grid_x, (num_heads + heads_per_wg - 1) / heads_per_wg);
+  // The fused merge: one workgroup per compute unit at most (the kernel's LDS
+  // use admits one), so that siblings normally run side by side.
+  p.fused = mode == 1 && (int64_t)p.grid.x * p.grid.y <= cus && mid_o_bytes < (size_t)INT32_MAX;
+  return p;
 }
 
 struct Common {
@@ -1703,7 +1749,7 @@ extern "C" {
 
 const char* tmla_last_error(void) { return g_err; }
 
-int tmla_version(void) { return 101; }
+int tmla_version(void) { return 200; }
 
 size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v, int32_t num_splits,
                             int32_t num_workers) {
@@ -1727,7 +1773,8 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
                   int64_t bt_stride_b, int32_t bt_cols, const int32_t* seqlens, int32_t batch, int32_t num_heads,
                   int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale, int32_t num_splits,
                   int32_t num_workers, void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
-                  void* workspace, size_t workspace_bytes_, void* stream, int mode, int32_t q_len = 1) {
+                  void* workspace, size_t workspace_bytes_, void* stream, int mode, int32_t q_len = 1,
+                  int32_t spin_limit = -1) {
   const Common c{batch, num_heads, head_dim_v, rope_dim, dtype, num_splits, num_workers};
   int rc = check_common(c, workspace, workspace_bytes_);
   if (rc != TMLA_OK) return rc;
@@ -1779,34 +1826,24 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   const WsLayout wl = ws_layout(batch, num_heads, 512, num_splits, num_workers);
   a.mid_o = reinterpret_cast<short*>(ws + wl.o);
   a.mid_lse = reinterpret_cast<float*>(ws + wl.l);
-  a.m_count = reinterpret_cast<int32_t*>(ws + wl.cnt);
-  a.m_done = reinterpret_cast<int32_t*>(ws + wl.done);
-  a.m_flag = reinterpret_cast<int32_t*>(ws + wl.flag);
-  a.spin_limit = g_spin_limit;
+  // counters at the end of the caller's buffer (check_common: it holds
+  // wl.total bytes, a multiple of 256, so the block starts at or after
+  // wl.part_end)
+  const int64_t gy_ws = head_blocks(num_heads);
+  char* cnt = ws + ((workspace_bytes_ & ~(size_t)255) - wl.cnt_bytes);
+  a.m_count = reinterpret_cast<int32_t*>(cnt);
+  a.m_done = a.m_count + (int64_t)batch * gy_ws;
+  a.m_flag = a.m_done + (int64_t)batch * gy_ws;
+  a.spin_limit = spin_limit >= 0 ? spin_limit : kDefaultSpinLimit;
 
-  // blocks of 32 heads per workgroup (4 waves in every case)
-  int nhb = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
-  const int workers = num_splits > 0 ? batch * num_splits : num_workers;
-  // Upper bound of the 64-token tiles the call can hold (block-table width or
-  // dense capacity): balanced workers past it never get a range, so the grid
-  // stops there, and when the busy workgroups would leave compute units idle,
-  // fewer heads per workgroup (more, shorter workgroups: less Q to load, less
-  // MFMA work per sub-tile, smaller partial rows) use them. The single-launch
-  // merge keeps the head blocks its counters are laid out for.
   const int64_t cap_tokens = paged ? (int64_t)bt_cols * page_size : num_blocks;
-  const int64_t tile_bound = (int64_t)batch * ((cap_tokens + kTileTokens - 1) / kTileTokens);
-  const int grid_x = num_splits > 0 ? workers : (int)(tile_bound < workers ? (tile_bound > 0 ? tile_bound : 1) : workers);
-  if (mode != 1) {
-    const int64_t cus = current_cu_count();
-    while (nhb > 1 && (int64_t)grid_x * ((num_heads + 16 * nhb - 1) / (16 * nhb)) <= cus) nhb /= 2;
-  }
-  const int heads_per_wg = 32 * nhb;
-  dim3 grid(grid_x, (num_heads + heads_per_wg - 1) / heads_per_wg);
-  // The fused merge: one workgroup per compute unit at most (the kernel's LDS
-  // use admits one), so that siblings normally run side by side.
   const size_t mid_o_bytes = wl.l - wl.o;  // partial rows, 256-byte aligned
+  const LaunchPlan plan =
+      plan_launch(batch, num_heads, num_splits, num_workers, cap_tokens, mid_o_bytes, mode, current_cu_count());
+  const int nhb = plan.nhb;
+  const dim3 grid = plan.grid;
   a.mid_o_bytes = (int32_t)(mid_o_bytes < (size_t)INT32_MAX ? mid_o_bytes : 0);
-  a.fused = mode == 1 && (int64_t)grid.x * grid.y <= current_cu_count() && mid_o_bytes < (size_t)INT32_MAX ? 1 : 0;
+  a.fused = plan.fused ? 1 : 0;
   // one page per 32-token sub-tile (sub-tiles never straddle a page) and a
   // power-of-two page size: page slots and in-page rows by shifts and masks
   const bool uni = paged && (page_size % kSubTokens == 0) && a.page_shift >= 0;
@@ -1888,11 +1925,30 @@ int tmla_mla_decode_fused(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           int64_t bt_stride_b, int32_t bt_cols, const int32_t* seqlens, int32_t batch,
                           int32_t num_heads, int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale,
                           int32_t num_splits, int32_t num_workers, void* out, int64_t out_stride_b,
-                          int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes_, void* stream) {
+                          int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes_,
+                          int32_t spin_limit, void* stream) {
   return decode_launch(q, q_stride_b, q_stride_h, kv, kv_stride_0, kv_stride_1, num_blocks, page_size, block_table,
                        bt_stride_b, bt_cols, seqlens, batch, num_heads, head_dim_v, rope_dim, dtype, softmax_scale,
                        num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace, workspace_bytes_,
-                       stream, 1);
+                       stream, 1, 1, spin_limit);
+}
+
+size_t tmla_workspace_zero_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v, int32_t num_splits,
+                                 int32_t num_workers) {
+  if (batch < 0 || num_heads <= 0 || head_dim_v < 0) return 0;
+  // the counter block plus the slack of rounding the buffer size down to 256
+  return ws_layout(batch, num_heads, head_dim_v, num_splits, num_workers).cnt_bytes + 255;
+}
+
+int32_t tmla_mla_decode_fused_is_single(int32_t batch, int32_t num_heads, int32_t head_dim_v, int32_t num_splits,
+                                        int32_t num_workers, int64_t capacity_tokens, int32_t device) {
+  if (batch <= 0 || num_heads <= 0 || head_dim_v != 512 || num_splits < 0 ||
+      (num_splits == 0 && num_workers <= 0))
+    return 0;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
+  const WsLayout wl = ws_layout(batch, num_heads, head_dim_v, num_splits, num_workers);
+  return plan_launch(batch, num_heads, num_splits, num_workers, capacity_tokens, wl.l - wl.o, 1, cus).fused ? 1 : 0;
 }
 
 int tmla_mla_decode_causal(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
@@ -1908,12 +1964,6 @@ int tmla_mla_decode_causal(const void* q, int64_t q_stride_b, int64_t q_stride_h
                        bt_stride_b, bt_cols, seqlens, batch, q_len * num_heads, head_dim_v, rope_dim, dtype,
                        softmax_scale, num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace,
                        workspace_bytes_, stream, single_launch ? 1 : 2, q_len);
-}
-
-int32_t tmla_set_merge_spin_limit(int32_t polls) {
-  const int32_t prev = g_spin_limit;
-  if (polls >= 0) g_spin_limit = polls;
-  return prev;
 }
 
 }  // extern "C"

@@ -24,7 +24,8 @@ SIGNATURES = {
     "tmla_version": (ctypes.c_int, []),
     "tmla_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "tmla_device_cu_count": (_i32, [_i32]),
-    "tmla_set_merge_spin_limit": (_i32, [_i32]),
+    "tmla_workspace_zero_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "tmla_mla_decode_fused_is_single": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64, _i32]),
     "tmla_mla_decode_partial": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
         _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
@@ -35,7 +36,7 @@ SIGNATURES = {
         _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "tmla_mla_decode_fused": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
-        _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+        _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _i32, _vp]),
     "tmla_mla_decode_causal": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32,
         _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _i32, _vp]),

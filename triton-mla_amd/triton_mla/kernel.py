@@ -57,6 +57,13 @@ def get_num_splits(batch, num_heads, max_seqlen, num_sms, min_tokens_per_split=1
     return 1 << (splits.bit_length() - 1)
 
 
+# The form mla_decode runs when single_launch is None: False = the two
+# kernels of the reference's scheme (partial, then combine), True = the single
+# launch (the merge inside the partial kernel, same bits) whenever its
+# workgroups fit on the device at once.
+DEFAULT_SINGLE_LAUNCH = False
+
+
 def _aligned(t: torch.Tensor) -> bool:
     return t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:-1])
 
@@ -149,14 +156,22 @@ class DecodeLaunch:
         # balanced partition: one worker per compute unit unless asked otherwise
         self.workers = 0 if num_splits is not None else int(num_workers or _num_sms(device))
         self.ws_bytes = self.lib.tmla_workspace_bytes(batch, vheads, head_dim_v, self.splits, self.workers)
-        # zero-filled once: the fused merge's counters start at zero and every
-        # call leaves them at zero
-        self.workspace = torch.zeros(max(self.ws_bytes, 1), dtype=torch.uint8, device=device)
+        # Uninitialised like the reference's buffers (kernel.py:268-271): the
+        # two-kernel form writes every byte it reads. Only the single launch's
+        # merge counters (a small block at the end) must start at zero; they
+        # are cleared before the first single launch and every launch leaves
+        # them at zero again.
+        self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=device)
+        self._zero_bytes = min(self.lib.tmla_workspace_zero_bytes(batch, vheads, head_dim_v, self.splits,
+                                                                  self.workers), self.ws_bytes)
+        self._counters_clear = False
         # run(single_launch=True) merges inside the partial kernel (one launch)
-        # when all of its workgroups fit on the device at once, one per CU
-        per_wg = 32 if vheads <= 32 else 64 if vheads <= 64 else 128
-        grid = (batch * self.splits if self.splits else self.workers) * -(-vheads // per_wg)
-        self.fused = grid <= _num_sms(device)
+        # when all of its workgroups fit on the device at once, one per CU: the
+        # library's own decision for these arguments
+        capacity = (block_table.shape[1] * page_size) if block_table is not None else num_blocks
+        self.fused = bool(self.lib.tmla_mla_decode_fused_is_single(
+            batch, vheads, head_dim_v, self.splits, self.workers, capacity,
+            device.index if device.index is not None else torch.cuda.current_device()))
         out_sh = self.out.stride(-2)  # one output row per (query token, head)
         self._partial_args = (
             q.data_ptr(), q.stride(0), q.stride(1),
@@ -194,17 +209,32 @@ class DecodeLaunch:
                 _native.check(self.lib.tmla_mla_decode_combine(*self._combine_args, self._stream()),
                               "tmla_mla_decode_combine")
 
-    def run(self, single_launch=False):
+    def _clear_counters(self):
+        if not self._counters_clear:
+            if self._zero_bytes > 0:
+                self.workspace[self.ws_bytes - self._zero_bytes:self.ws_bytes].zero_()
+            self._counters_clear = True
+
+    def run(self, single_launch=False, spin_limit=-1):
         """Both stages (tmla_mla_decode), or the single-launch form
-        (tmla_mla_decode_fused) when single_launch is set."""
+        (tmla_mla_decode_fused) when single_launch is set. spin_limit: polls
+        a worker of the in-kernel merge waits for its siblings before it hands
+        its share over (< 0: the library's default)."""
         if self.batch and self.q_len > 1:
             with torch.cuda.device(self.device):
+                if single_launch:
+                    self._clear_counters()
                 _native.check(self.lib.tmla_mla_decode_causal(*self._causal_args, int(bool(single_launch)),
                                                               self._stream()), "tmla_mla_decode_causal")
         elif self.batch:
-            name = "tmla_mla_decode_fused" if single_launch else "tmla_mla_decode"
             with torch.cuda.device(self.device):
-                _native.check(getattr(self.lib, name)(*self._partial_args, self._stream()), name)
+                if single_launch:
+                    self._clear_counters()
+                    _native.check(self.lib.tmla_mla_decode_fused(*self._partial_args, int(spin_limit),
+                                                                 self._stream()), "tmla_mla_decode_fused")
+                else:
+                    _native.check(self.lib.tmla_mla_decode(*self._partial_args, self._stream()),
+                                  "tmla_mla_decode")
         return self.out, self.lse
 
 
@@ -217,7 +247,7 @@ def mla_decode(
     softmax_scale: float = None,
     num_splits: int = None,
     return_lse: bool = False,
-    single_launch: bool = False,
+    single_launch: bool = None,
 ):
     """Weight-absorbed MLA decode attention over a shared latent KV cache.
 
@@ -243,14 +273,14 @@ def mla_decode(
         return_lse: also return the natural-log log-sum-exp per head.
         single_launch: merge the split partials inside the partial kernel
             (one launch instead of two, same bits) when its workgroups fit on
-            the device at once.
+            the device at once; None selects DEFAULT_SINGLE_LAUNCH.
 
     Returns:
         out [batch, num_heads, head_dim_v] in q.dtype (and lse [batch,
         num_heads] float32).
     """
     call = DecodeLaunch(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits)
-    out, lse = call.run(single_launch)
+    out, lse = call.run(DEFAULT_SINGLE_LAUNCH if single_launch is None else single_launch)
     if return_lse:
         return out, lse
     return out

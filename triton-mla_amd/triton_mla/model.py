@@ -20,7 +20,6 @@ from dataclasses import dataclass
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import layer_ops
 from .kernel import mla_decode
@@ -49,13 +48,22 @@ class MLAConfig:
 
 
 class RMSNorm(nn.Module):
+    """Root-mean-square normalisation with a learned gain (model.py:34-41).
+
+    Computed in float32 and rounded once to the input dtype: y = x / rms(x)
+    * weight with rms(x) = sqrt(mean(x^2) + eps), the same arithmetic as the
+    HIP cache-append kernel's normalisation of the latent.
+    """
+
     def __init__(self, dim, eps=1e-6):
         super().__init__()
-        self.eps = eps
         self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
 
     def forward(self, x):
-        return F.rms_norm(x, (x.shape[-1],), self.weight, self.eps)
+        xf = x.float()
+        inv_rms = torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + self.eps)
+        return (xf * inv_rms * self.weight.float()).to(x.dtype)
 
 
 def apply_rope(x, positions, theta):
@@ -87,33 +95,47 @@ class MLA(nn.Module):
         self.softmax_scale = cfg.qk_head_dim ** -0.5
 
     def _project(self, x, positions):
+        """Query and latent of the new token (model.py:74-82): q_nope
+        [B, H, nope], RoPE'd q_pe [B, H, rope], normalised latent c_kv
+        [B, rank] and RoPE'd shared key k_pe [B, rope]."""
         cfg = self.cfg
-        q = self.wq_b(self.q_norm(self.wq_a(x))).view(x.shape[0], cfg.num_heads, cfg.qk_head_dim)
-        q_nope, q_pe = q.split([cfg.qk_nope_head_dim, cfg.qk_rope_head_dim], dim=-1)
-        q_pe = apply_rope(q_pe, positions[:, None], cfg.rope_theta)
-        c_kv, k_pe = self.wkv_a(x).split([cfg.kv_lora_rank, cfg.qk_rope_head_dim], dim=-1)
-        c_kv = self.kv_norm(c_kv)
-        k_pe = apply_rope(k_pe, positions, cfg.rope_theta)
+        q_lat = self.q_norm(self.wq_a(x))
+        q = self.wq_b(q_lat).unflatten(-1, (cfg.num_heads, cfg.qk_head_dim))
+        q_nope = q[..., :cfg.qk_nope_head_dim]
+        q_pe = apply_rope(q[..., cfg.qk_nope_head_dim:], positions.unsqueeze(-1), cfg.rope_theta)
+        kv = self.wkv_a(x)
+        c_kv = self.kv_norm(kv[..., :cfg.kv_lora_rank])
+        k_pe = apply_rope(kv[..., cfg.kv_lora_rank:], positions, cfg.rope_theta)
         return q_nope, q_pe, c_kv, k_pe
 
     @staticmethod
     def _append_kv(kv_cache, c_kv, k_pe, cache_seqlens, block_table):
-        """Write each sequence's new latent row at position cache_seqlens[b]."""
-        entry = torch.cat([c_kv, k_pe], dim=-1).to(kv_cache.dtype)
-        pos = cache_seqlens.long()
-        rows = torch.arange(pos.shape[0], device=pos.device)
+        """Store each sequence's new cache row [c_kv, k_pe] at token position
+        cache_seqlens[b] (model.py:84-94): through the block table for a paged
+        cache, at row b of a dense one."""
+        width = kv_cache.shape[-1]
+        rows = torch.cat([c_kv, k_pe], dim=-1).to(kv_cache.dtype)
+        pos = cache_seqlens.to(torch.int64)
+        per_block = kv_cache.shape[1]  # tokens per page, or the dense capacity
         if block_table is None:
-            kv_cache[rows, pos] = entry
+            block = torch.arange(pos.numel(), device=pos.device)
+            slot = pos
         else:
-            page_size = kv_cache.shape[1]
-            pages = block_table[rows, pos // page_size].long()
-            kv_cache[pages, pos % page_size] = entry
+            block = block_table.gather(1, (pos // per_block).unsqueeze(1)).squeeze(1).to(torch.int64)
+            slot = pos % per_block
+        flat_index = block * per_block + slot
+        if kv_cache.is_contiguous():
+            kv_cache.view(-1, width).index_copy_(0, flat_index, rows)
+        else:
+            kv_cache[block, slot] = rows
 
     def _wkv_b(self):
-        """(W_UK [H, nope, rank], W_UV [H, v, rank]) views of wkv_b."""
+        """W_UK [H, nope, rank] and W_UV [H, v, rank]: the per-head row blocks
+        of wkv_b (model.py:96-99)."""
         cfg = self.cfg
-        w = self.wkv_b.weight.view(cfg.num_heads, cfg.qk_nope_head_dim + cfg.v_head_dim, cfg.kv_lora_rank)
-        return w[:, : cfg.qk_nope_head_dim], w[:, cfg.qk_nope_head_dim:]
+        per_head = self.wkv_b.weight.unflatten(0, (cfg.num_heads, cfg.qk_nope_head_dim + cfg.v_head_dim))
+        w_uk, w_uv = torch.split(per_head, [cfg.qk_nope_head_dim, cfg.v_head_dim], dim=1)
+        return w_uk, w_uv
 
     def forward(self, x, kv_cache, cache_seqlens, block_table=None, num_splits=None):
         """One decode step for x [batch, hidden].
@@ -122,8 +144,10 @@ class MLA(nn.Module):
         (output [batch, hidden], updated cache_seqlens).
         """
         cfg = self.cfg
-        if kv_cache.dtype != x.dtype:
-            raise NotImplementedError("MLA.forward needs the cache in the layer's dtype")
+        if kv_cache.dtype != x.dtype or x.dtype not in (torch.bfloat16, torch.float16):
+            # the HIP glue runs in the layer's 16-bit dtype; other dtype mixes
+            # take the reference's torch glue, which casts (model.py:108-124)
+            return self.forward_torch_glue(x, kv_cache, cache_seqlens, block_table, num_splits)
         q_proj = self.wq_b(self.q_norm(self.wq_a(x)))  # [B, H * (nope + rope)]
         kv_proj = self.wkv_a(x)  # [B, rank + rope]
         # RMSNorm(c_kv), RoPE(k_pe) and the paged append (model.py:80-94)
@@ -159,20 +183,25 @@ class MLA(nn.Module):
         return self.wo(o.flatten(1)), seqlens
 
     def forward_naive(self, x, kv_cache, cache_seqlens, block_table=None):
-        """Same decode step without absorption: decompress the cache into per-head K/V."""
+        """The same decode step without absorption (model.py:126-144): every
+        cached latent is expanded through wkv_b into per-head keys and values,
+        and attention runs per head in float32. The layer's oracle."""
         cfg = self.cfg
         q_nope, q_pe, c_kv, k_pe = self._project(x, cache_seqlens)
         self._append_kv(kv_cache, c_kv, k_pe, cache_seqlens, block_table)
         seqlens = cache_seqlens + 1
-        kv = gather_kv(kv_cache, seqlens, block_table).to(x.dtype)
-        latent, kpe = kv.split([cfg.kv_lora_rank, cfg.qk_rope_head_dim], dim=-1)
-        kvb = self.wkv_b(latent).view(*latent.shape[:2], cfg.num_heads, -1)
-        k_nope, v = kvb.split([cfg.qk_nope_head_dim, cfg.v_head_dim], dim=-1)
-        k = torch.cat([k_nope, kpe[:, :, None].expand(-1, -1, cfg.num_heads, -1)], dim=-1)
-        q = torch.cat([q_nope, q_pe], dim=-1)
-        # scores [B, H, S] and output [B, H, v] in float32
-        scores = torch.einsum("bhd,bshd->bhs", q.float(), k.float()) * self.softmax_scale
-        invalid = torch.arange(kv.shape[1], device=x.device)[None, :] >= seqlens[:, None]
-        scores = scores.masked_fill(invalid[:, None, :], float("-inf"))
-        o = torch.einsum("bhs,bshd->bhd", scores.softmax(-1), v.float()).to(x.dtype)
+        cache = gather_kv(kv_cache, seqlens, block_table).to(x.dtype)  # [B, S, rank + rope]
+        latent = cache[..., :cfg.kv_lora_rank]
+        shared_k = cache[..., cfg.kv_lora_rank:].float()  # [B, S, rope], one key for all heads
+        expanded = self.wkv_b(latent).unflatten(-1, (cfg.num_heads, cfg.qk_nope_head_dim + cfg.v_head_dim))
+        k_heads = expanded[..., :cfg.qk_nope_head_dim].float().permute(0, 2, 3, 1).contiguous()  # [B, H, nope, S]
+        v_heads = expanded[..., cfg.qk_nope_head_dim:].float().permute(0, 2, 1, 3).contiguous()  # [B, H, S, v]
+        # per-head content scores plus the shared positional scores
+        scores = torch.matmul(q_nope.float().unsqueeze(2), k_heads).squeeze(2)  # [B, H, S]
+        scores = scores + torch.matmul(q_pe.float(), shared_k.transpose(1, 2).contiguous())
+        scores = scores * self.softmax_scale
+        past_end = torch.arange(cache.shape[1], device=x.device).unsqueeze(0) >= seqlens.unsqueeze(1)
+        scores = scores.masked_fill(past_end.unsqueeze(1), float("-inf"))
+        weights = torch.softmax(scores, dim=-1)
+        o = torch.matmul(weights.unsqueeze(2), v_heads).squeeze(2).to(x.dtype)  # [B, H, v]
         return self.wo(o.flatten(1)), seqlens
