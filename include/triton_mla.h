@@ -160,6 +160,28 @@ int tmla_mla_decode_fused(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           int32_t spin_limit, void* stream);
 
 /*
+ * tmla_mla_decode without a caller-owned workspace: no counterpart in the
+ * reference (whose launches take buffers torch allocates per call,
+ * kernel.py:268-271). For callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The partials live in a 64 MiB device array built into the
+ * library, one per device, held until the process ends; no call allocates or
+ * frees anything. Calls whose tmla_workspace_bytes exceed 64 MiB return
+ * TMLA_ERR_WORKSPACE_TOO_SMALL before touching the device. Every call on a
+ * device shares that device's array: calls that overlap on one device (other
+ * streams, other threads) race and must be serialised by the caller. The
+ * stream must belong to the current device. Results equal tmla_mla_decode's
+ * bit for bit.
+ */
+int tmla_mla_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                            int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks,
+                            int32_t page_size, const int32_t* block_table, int64_t bt_stride_b,
+                            int32_t bt_cols, const int32_t* seqlens, int32_t batch, int32_t num_heads,
+                            int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale,
+                            int32_t num_splits, int32_t num_workers, void* out, int64_t out_stride_b,
+                            int64_t out_stride_h, float* lse, void* stream);
+
+/*
  * 1 when tmla_mla_decode_fused with these arguments runs as a single launch
  * on `device`, 0 when it runs both stages. capacity_tokens = bt_cols *
  * page_size for a paged cache, the dense capacity otherwise (the launch

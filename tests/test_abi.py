@@ -134,3 +134,13 @@ def test_layer_glue_arguments_rejected_on_host(lib):
     assert lib.tmla_mla_kv_append(*args) == 1 and b"page_size" in lib.tmla_last_error()
     args = list(k); args[13] = 0
     assert lib.tmla_mla_kv_append(*args) == 1
+
+
+def test_noalloc_rejects_calls_beyond_the_scratch(lib):
+    # no device is touched: the workspace the call would need is checked first
+    fake = ctypes.c_void_p(1 << 20)
+    need = lib.tmla_workspace_bytes(64, 512, 512, 0, 256)
+    assert need > 64 << 20
+    rc = lib.tmla_mla_decode_noalloc(fake, 512 * 576, 576, fake, 64 * 576, 576, 8, 64, fake, 1, 1, fake, 64, 512,
+                                     512, 64, 0, 0.1, 0, 256, fake, 512 * 512, 512, fake, None)
+    assert rc == 3 and b"built-in scratch" in lib.tmla_last_error()

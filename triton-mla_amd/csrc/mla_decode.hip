@@ -33,6 +33,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 #include <utility>
 
 #include "cdna.h"
@@ -1857,6 +1858,49 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   return TMLA_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Built-in workspace of tmla_mla_decode_noalloc: a device array of fixed size
+// that the code object carries, so that callers that may not allocate
+// (code under HIP graph capture, serving loops, harnesses that forbid
+// hipMalloc) can still run the two-kernel decode. Each device that loads the
+// library holds its own copy until the process ends. Host code never passes
+// the array's name to a kernel (on the host it is a stand-in, not a device
+// address): its per-device address comes from hipGetSymbolAddress, once per
+// device, with that device current.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The address of `scratch` on the device `stream` belongs to (the current
+// device for the null stream), which must be the current device.
+int scratch_for_stream(void* stream, void** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t sd = 0;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sd);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamGetDevice");
+    dev = (int)sd;
+  }
+  if (dev != cur) return fail(TMLA_ERR_INVALID_ARGUMENT, "stream belongs to a device other than the current one");
+  if (dev < 0 || dev >= kMaxDevices) return fail(TMLA_ERR_UNSUPPORTED, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TMLA_OK;
+}
+
 }  // namespace tmla
 
 extern "C" {
@@ -1931,6 +1975,29 @@ int tmla_mla_decode_fused(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                        bt_stride_b, bt_cols, seqlens, batch, num_heads, head_dim_v, rope_dim, dtype, softmax_scale,
                        num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace, workspace_bytes_,
                        stream, 1, 1, spin_limit);
+}
+
+int tmla_mla_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                            int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
+                            const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols,
+                            const int32_t* seqlens, int32_t batch, int32_t num_heads, int32_t head_dim_v,
+                            int32_t rope_dim, int32_t dtype, float softmax_scale, int32_t num_splits,
+                            int32_t num_workers, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                            float* lse, void* stream) {
+  const size_t need = workspace_bytes(batch, num_heads, head_dim_v, num_splits, num_workers);
+  if (need > kScratchBytes) {
+    snprintf(g_err, sizeof(g_err),
+             "the call needs %zu bytes of workspace, more than the %zu of the built-in scratch "
+             "(use tmla_mla_decode with a caller-owned workspace)",
+             need, kScratchBytes);
+    return TMLA_ERR_WORKSPACE_TOO_SMALL;
+  }
+  void* ws = nullptr;
+  const int rc = scratch_for_stream(stream, &ws);
+  if (rc != TMLA_OK) return rc;
+  return decode_launch(q, q_stride_b, q_stride_h, kv, kv_stride_0, kv_stride_1, num_blocks, page_size, block_table,
+                       bt_stride_b, bt_cols, seqlens, batch, num_heads, head_dim_v, rope_dim, dtype, softmax_scale,
+                       num_splits, num_workers, out, out_stride_b, out_stride_h, lse, ws, kScratchBytes, stream, 2);
 }
 
 size_t tmla_workspace_zero_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v, int32_t num_splits,

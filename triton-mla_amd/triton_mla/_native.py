@@ -37,6 +37,9 @@ SIGNATURES = {
     "tmla_mla_decode_fused": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
         _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _i32, _vp]),
+    "tmla_mla_decode_noalloc": (ctypes.c_int, [
+        _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
+        _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp]),
     "tmla_mla_decode_causal": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32,
         _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _i32, _vp]),
