@@ -217,6 +217,16 @@ int tmla_mla_decode_causal(const void* q, int64_t q_stride_b, int64_t q_stride_h
                            float softmax_scale, int32_t num_splits, int32_t num_workers, void* out,
                            int64_t out_stride_b, int64_t out_stride_h, float* lse, void* workspace,
                            size_t workspace_bytes, int32_t single_launch, void* stream);
+/*
+ * Profiling hook, no counterpart in the reference: copies the partial
+ * kernel's phase stamps of the last launch into `host` (up to `bytes`):
+ * 4096 workers x 9 slots x {100 MHz wall clock, shader clock} uint64 (slot
+ * meanings in mla_decode.hip, phase_stamp). Synchronous. Only a library
+ * built with TMLA_STAMPS=1 records stamps; any other build returns
+ * TMLA_ERR_UNSUPPORTED.
+ */
+int tmla_debug_stamps(void* host, size_t bytes);
+
 /* Number of compute units of `device` (0 on error); the default worker count. */
 int32_t tmla_device_cu_count(int32_t device);
 

@@ -1,6 +1,8 @@
 """Build the HIP kernels of triton_mla into an in-tree shared library.
 
     python triton-mla_amd/build.py            # compile for gfx950
+    python triton-mla_amd/build.py --stamps   # profiling build with phase stamps
+                                              # (libtriton_mla_hip_stamps.so)
 
 The library is a plain C-ABI ``.so`` (declarations in include/triton_mla.h)
 that the Python package loads with ctypes. It links against the HIP runtime
@@ -20,6 +22,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "triton_mla", "libtriton_mla_hip.so")
+LIB_STAMPS = os.path.join(HERE, "triton_mla", "libtriton_mla_hip_stamps.so")
 SOURCES = ["mla_decode.hip", "mla_layer.hip"]
 ARCH = os.environ.get("TRITON_MLA_ARCH", "gfx950")
 
@@ -31,24 +34,26 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source into LIB; always recompiles. Returns the path."""
+def build(verbose: bool = False, stamps: bool = False) -> str:
+    """Compile every HIP source into LIB (or, with stamps, the phase-stamp
+    profiling build LIB_STAMPS); always recompiles. Returns the path."""
+    out = LIB_STAMPS if stamps else LIB
     cmd = [
         hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
         "-mcode-object-version=5",
         # packed fp32 VALU forms are kept out of every kernel on this target
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        f"-I{INCLUDE}", "-o", LIB + ".tmp",
-    ] + [os.path.join(CSRC, s) for s in SOURCES]
+        f"-I{INCLUDE}", "-o", out + ".tmp",
+    ] + (["-DTMLA_STAMPS=1"] if stamps else []) + [os.path.join(CSRC, s) for s in SOURCES]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed ({res.returncode})")
-    check_kernel_stubs(LIB + ".tmp")
-    os.replace(LIB + ".tmp", LIB)
-    return LIB
+    check_kernel_stubs(out + ".tmp")
+    os.replace(out + ".tmp", out)
+    return out
 
 
 def check_kernel_stubs(path: str) -> None:
@@ -69,4 +74,4 @@ def check_kernel_stubs(path: str) -> None:
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, stamps="--stamps" in sys.argv[1:]))

@@ -77,6 +77,10 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 #ifndef TMLA_WAIT_PAIR
 #define TMLA_WAIT_PAIR 1
 #endif
+// 1: phase stamps (profiling builds only; see tmla_debug_stamps)
+#ifndef TMLA_STAMPS
+#define TMLA_STAMPS 0
+#endif
 constexpr int kStages = 4;          // LDS ring depth (3 sub-tiles in flight)
 constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (p <= 2^8)
@@ -133,6 +137,46 @@ struct CombineArgs {
 // ---------------------------------------------------------------------------
 // small device helpers
 // ---------------------------------------------------------------------------
+
+// Phase stamps of a profiling build (TMLA_STAMPS=1): lane 0 of wave 0 of
+// workgroups (x, 0), x < kStampWorkers, stores the 100 MHz wall clock and the
+// shader clock when it reaches a phase: 0 entry, 1 work range known, 2 loop
+// start, 3 loop end, 4 finalize end of its first segment, and inside
+// iteration kStampIter of that segment 5 start (after the barrier), 6 after
+// the first pass, 7 after the second pass, 8 start of the next iteration.
+// Compiled out otherwise.
+constexpr int kStampWorkers = 4096;
+constexpr int kStampSlots = 9;
+constexpr int kStampIter = 8;
+#if TMLA_STAMPS
+__device__ unsigned long long g_stamps[kStampWorkers * kStampSlots * 2];
+#endif
+// The clocks are read where the phase is reached (stamp_now) and stored
+// later (stamp_store), where the code waits for its LDS and scalar
+// operations anyway, so reading them adds no wait inside a phase.
+struct StampRec {
+  unsigned long long rt, ck;
+};
+__device__ __forceinline__ StampRec stamp_now() {
+#if TMLA_STAMPS
+  return StampRec{__builtin_amdgcn_s_memrealtime(), __builtin_amdgcn_s_memtime()};
+#else
+  return StampRec{0, 0};
+#endif
+}
+__device__ __forceinline__ void stamp_store(int slot, StampRec r) {
+#if TMLA_STAMPS
+  if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < kStampWorkers) {
+    unsigned long long* p = g_stamps + ((size_t)blockIdx.x * kStampSlots + slot) * 2;
+    asm volatile("global_store_dwordx2 %0, %1, off" : : "v"(p), "v"(r.rt) : "memory");
+    asm volatile("global_store_dwordx2 %0, %1, off offset:8" : : "v"(p), "v"(r.ck) : "memory");
+  }
+#else
+  (void)slot;
+  (void)r;
+#endif
+}
+__device__ __forceinline__ void phase_stamp(int slot) { stamp_store(slot, stamp_now()); }
 
 __device__ __forceinline__ int tiles_of(int n) { return n > 0 ? (n + kTileTokens - 1) / kTileTokens : 0; }
 
@@ -291,6 +335,27 @@ __device__ __forceinline__ void mfma_vgpr_acc(f32x16& d, const i16x8& a, const i
 }
 __device__ __forceinline__ void mfma_vgpr_fence(f32x16& d) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(d));
+}
+
+// Two probabilities rounded to the 16-bit type, packed into one dword (a in
+// the low half). The softmax packs its 16 probabilities in place into the
+// first 8 registers of the score tile (pair k reads registers 2k and 2k + 1,
+// which no earlier pair has overwritten), so P^T needs no registers of its
+// own: registers 0-3 hold the first token half, 4-7 the second.
+template <int DT>
+__device__ __forceinline__ float pack_pair(float a, float b) {
+  const unsigned lo = (unsigned short)Elt<DT>::from_float(a), hi = (unsigned short)Elt<DT>::from_float(b);
+  return __builtin_bit_cast(float, lo | (hi << 16));
+}
+template <int DT>
+__device__ __forceinline__ void pack_probs_in_place(f32x16& p) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) p[k] = pack_pair<DT>(p[2 * k], p[2 * k + 1]);
+  pin_f16(p);
+}
+__device__ __forceinline__ i16x8 packed_half(const f32x16& p, int h) {
+  const f32x4 v = h == 0 ? f32x4{p[0], p[1], p[2], p[3]} : f32x4{p[4], p[5], p[6], p[7]};
+  return __builtin_bit_cast(i16x8, v);
 }
 
 // 16-byte store written through to memory (sc0 sc1: system-scope write-
@@ -696,6 +761,7 @@ void mla_partial_kernel(PartialArgs a) {
   __shared__ int s_pend[2][5];
   __shared__ int s_msg[4];
 
+  phase_stamp(0);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar LDS bases
   // Logical worker index: consecutive workers (the pieces of one sequence,
@@ -824,6 +890,7 @@ void mla_partial_kernel(PartialArgs a) {
     }
   }
   if (tile_lo >= tile_hi) return;
+  phase_stamp(1);
 
   // ---- segments -----------------------------------------------------------
   int b = b_first;
@@ -847,16 +914,16 @@ void mla_partial_kernel(PartialArgs a) {
     const int hi = lane >> 5;  // which half of the 32-token M block / k slots
     // per-lane LDS read offsets inside a ring entry
     // S^T A operand: token = lane%32 (rg = (lane%32)/8, r = lane%8), piece = 2*(kc%4) + hi
-    int k_off_v[4], k_off_r[4];
+    // (the rope part's offset is the latent part's plus k_rope_delta: the
+    // two rings differ only in the row-group stride)
+    int k_off_v[4];
+    int k_rope_delta;
     {
       const int rg = (lane & 31) >> 3, r = lane & 7;
       const int sw = piece_swizzle(r, rg);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int in_block = (r * 8 + ((2 * j + hi) ^ sw)) * 16;
-        k_off_v[j] = rg * NVB * 1024 + in_block;
-        k_off_r[j] = OFF_R + rg * NRB * 1024 + in_block;
-      }
+      for (int j = 0; j < 4; ++j) k_off_v[j] = rg * NVB * 1024 + (r * 8 + ((2 * j + hi) ^ sw)) * 16;
+      k_rope_delta = OFF_R - rg * (NVB - NRB) * 1024;
     }
     // V^T operand via ds_read_b64_tr_b16: group g = lane/16, L = lane%16;
     // read e2 covers tokens 16c + 8e2 + 4(g/2) + L/4, dims 32db + 16(g%2) + 4(L%4).
@@ -950,11 +1017,12 @@ void mla_partial_kernel(PartialArgs a) {
     // partial one) needs no clamping: its rows start at a uniform offset
     // (page, first row in the page) plus a per-lane offset that is the same
     // for every sub-tile of the segment.
-    int64_t lane_row_off[RG_PER_WAVE];
+    // (32 rows of one page: below 2^31 bytes, which the host checks)
+    uint32_t lane_row_off[RG_PER_WAVE];
 #pragma unroll
     for (int ri = 0; ri < RG_PER_WAVE; ++ri) {
       const int rg = wave * RG_PER_WAVE + ri;
-      lane_row_off[ri] = (int64_t)(rg * 8 + dma_r) * a.kv_s1 + ((lane & 7) ^ piece_swizzle(dma_r, rg)) * 16;
+      lane_row_off[ri] = (uint32_t)((rg * 8 + dma_r) * (uint32_t)a.kv_s1) + ((lane & 7) ^ piece_swizzle(dma_r, rg)) * 16;
     }
     auto copy_src = [&](int st, int page, const char* (&src)[RG_PER_WAVE]) __attribute__((always_inline)) {
       const int tok_base = st * kSubTokens;
@@ -1021,19 +1089,23 @@ void mla_partial_kernel(PartialArgs a) {
     constexpr int PV_STRIDE0 = (NKC - 1 - PV_START) / (PV_SPLIT > 1 ? PV_SPLIT - 1 : 1);
     constexpr int PV_STRIDE = TMLA_PV_STRIDE < PV_STRIDE0 ? TMLA_PV_STRIDE : (PV_STRIDE0 > 0 ? PV_STRIDE0 : 1);
     static_assert(NDBW == 4, "four 32-dim blocks per wave");
-    auto pass = [&](auto DOS, auto PVLO, auto PVHI, auto PVOFFC, auto PVSC, auto MINSTEPS, const char LDS_AS* kst_v,
-                    const char LDS_AS* kst_r, const char LDS_AS* vst, const char LDS_AS* pst, f32x16& s, auto&& hook)
-                    __attribute__((always_inline)) {
-      constexpr bool do_s = decltype(DOS)::value;
+    // S runs k-steps [SLO, SHI) of the S^T chain (the whole chain: [0, NKC));
+    // the fence after its last k-step makes the scores readable by VALU.
+    auto pass = [&](auto SLOC, auto SHIC, auto PVLO, auto PVHI, auto PVOFFC, auto PVSC, auto MINSTEPS,
+                    const char LDS_AS* kst_v, const char LDS_AS* kst_r, const char LDS_AS* vst, const char LDS_AS* pst,
+                    f32x16& s, auto&& hook) __attribute__((always_inline)) {
+      constexpr int SLO = decltype(SLOC)::value, SHI = decltype(SHIC)::value;
+      constexpr bool do_s = SHI > SLO;
       constexpr int PV0 = decltype(PVLO)::value;
       constexpr int PVOFF = decltype(PVOFFC)::value;
       constexpr int PVS = decltype(PVSC)::value;
-      constexpr int NS = do_s ? NKC : 0, NV = decltype(PVHI)::value - PV0;
+      constexpr int NS = SHI - SLO, NV = decltype(PVHI)::value - PV0;
       constexpr int PV_END = PVOFF + (NV - 1) * PVS + 1;  // one past the last PV step
       constexpr int NSTEPS0 = NS > PV_END ? NS : PV_END;
       constexpr int NSTEPS = NSTEPS0 > decltype(MINSTEPS)::value ? NSTEPS0 : decltype(MINSTEPS)::value;
       const char LDS_AS* kvb[4] = {kst_v + k_off_v[0], kst_v + k_off_v[1], kst_v + k_off_v[2], kst_v + k_off_v[3]};
-      const char LDS_AS* krb[4] = {kst_r + k_off_r[0], kst_r + k_off_r[1], kst_r + k_off_r[2], kst_r + k_off_r[3]};
+      const int rope_shift = (int)(kst_r - kst_v) + k_rope_delta;
+      const char LDS_AS* krb[4] = {kvb[0] + rope_shift, kvb[1] + rope_shift, kvb[2] + rope_shift, kvb[3] + rope_shift};
       const char LDS_AS* vbase[2][2] = {{vst + v_off[0][0], vst + v_off[0][1]},
                                         {vst + v_off[1][0], vst + v_off[1][1]}};
       const char LDS_AS* pbase = pst + lane * 16;
@@ -1042,11 +1114,11 @@ void mla_partial_kernel(PartialArgs a) {
       auto fetch = [&](auto T) __attribute__((always_inline)) {
         constexpr int t = decltype(T)::value;
         if constexpr (t < NS) {
-          constexpr int cb = t >> 2;
+          constexpr int kc = SLO + t, cb = kc >> 2;
           if constexpr (cb < NVB)
-            kb[t % (PD + 1)] = ds_read_b128<cb * 1024>(kvb[t & 3]);
+            kb[t % (PD + 1)] = ds_read_b128<cb * 1024>(kvb[kc & 3]);
           else
-            kb[t % (PD + 1)] = ds_read_b128<(cb - NVB) * 1024>(krb[t & 3]);
+            kb[t % (PD + 1)] = ds_read_b128<(cb - NVB) * 1024>(krb[kc & 3]);
         }
         if constexpr (pass_has_pv(t, NV, PVOFF, PVS)) {
           constexpr int g = PV0 + (t - PVOFF) / PVS, c = g / SPC, j4 = (g % SPC) / NHB, hb = g % NHB;
@@ -1102,10 +1174,10 @@ void mla_partial_kernel(PartialArgs a) {
           }
         }
         if constexpr (j < NS) {
-          if constexpr (j == 0)
+          if constexpr (SLO + j == 0)
             s = mfma_vgpr_first<DT>(kb[0], qop[0]);
           else
-            mfma_vgpr_acc<DT>(s, kb[r], qop[j]);
+            mfma_vgpr_acc<DT>(s, kb[r], qop[SLO + j]);
         }
         if constexpr (pv) {
           const i16x4 lo = vl[vi], hi4 = vh[vi];
@@ -1115,7 +1187,7 @@ void mla_partial_kernel(PartialArgs a) {
         }
         hook(J);
       });
-      if constexpr (do_s) mfma_vgpr_fence(s);
+      if constexpr (do_s && SHI == NKC) mfma_vgpr_fence(s);
     };
 
     // PV side: O^T columns of head block hb scale by the factor its S-owner
@@ -1200,7 +1272,7 @@ void mla_partial_kernel(PartialArgs a) {
         for (int kc = 0; kc < NKC; ++kc) {
           const int cb = kc >> 2;
           const char LDS_AS* p = cb < NVB ? lds + wave * VSLOT + k_off_v[kc & 3] + cb * 1024
-                                          : lds + qrope - OFF_R + k_off_r[kc & 3] + (cb - NVB) * 1024;
+                                          : lds + qrope - OFF_R + k_off_v[kc & 3] + k_rope_delta + (cb - NVB) * 1024;
           qop[kc] = *reinterpret_cast<const i16x8 LDS_AS*>(p);
         }
       }
@@ -1281,6 +1353,9 @@ void mla_partial_kernel(PartialArgs a) {
       const int copy_roff = (int)(r1 == 0u ? 2u : r1 - 1u) * RSLOT;
       const char LDS_AS* pst = lds + OFF_P + pbuf * PSLOT;
       const int st_s = st0 + i + 1;  // sub-tile of this iteration's S
+      const bool stamped = TMLA_STAMPS && b == b_first && (i == kStampIter || i == kStampIter + 1);
+      StampRec st_begin{}, st_pass1{}, st_pass2{};
+      if (stamped) st_begin = stamp_now();
 
       // pass 1: S(i+1) and PV(i) steps [0, PV_SPLIT) from step PV_START on;
       // the copies of sub-tile i+3 are spread evenly over the pass's steps,
@@ -1318,14 +1393,15 @@ void mla_partial_kernel(PartialArgs a) {
       // -s (scale < 0) and the scale is folded into p = 2^(s * c - m).
       auto owner_iteration = [&]() __attribute__((always_inline)) {
         f32x16 s;
-        pass(std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
-             std::integral_constant<int, PV_START>{}, std::integral_constant<int, PV_STRIDE>{},
+        pass(std::integral_constant<int, 0>{}, std::integral_constant<int, NKC>{}, std::integral_constant<int, 0>{},
+             std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, PV_START>{},
+             std::integral_constant<int, PV_STRIDE>{},
              std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s, pass1_hook(std::integral_constant<int, NKC>{}));
+        if (stamped) st_pass1 = stamp_now();
         // no token past the sequence (for the wave's earliest query token)
         const bool full = (st_s + 1) * kSubTokens <= n_b - lag_wave;
         const float c = a.qk_scale_log2;
         float m_use = m_run, lsum = 0.0f, alpha = 1.0f;
-        i16x8 pnext[2];
         auto softmax_hook = [&](auto J) __attribute__((always_inline)) {
           constexpr int j = decltype(J)::value;
           if constexpr (j == 0) {  // mask tokens past the sequence (last sub-tile only)
@@ -1365,33 +1441,44 @@ void mla_partial_kernel(PartialArgs a) {
             pin_f16(s);
             pin_f1(lsum);
           } else if constexpr (j == 2 + 16 / EXP_PER_STEP) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) pnext[r >> 3][r & 7] = Elt<DT>::from_float(s[r]);
+            pack_probs_in_place<DT>(s);
           }
         };
-        pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * SPC>{},
-             std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, std::integral_constant<int, SM_STEPS>{},
-             kst_v, kst_r, vst, pst, s, softmax_hook);
+        pass(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
+             std::integral_constant<int, 2 * SPC>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{},
+             std::integral_constant<int, SM_STEPS>{}, kst_v, kst_r, vst, pst, s, softmax_hook);
+        if (stamped) st_pass2 = stamp_now();
         {
           char LDS_AS* pw = lds + OFF_P + (pbuf ^ 1) * PSLOT + wave * 2 * 1024 + lane * 16;
-          ds_write_b128<0>(pw, pnext[0]);
-          ds_write_b128<1024>(pw, pnext[1]);
+          ds_write_b128<0>(pw, packed_half(s, 0));
+          ds_write_b128<1024>(pw, packed_half(s, 1));
           ds_write_b32(lds + OFF_A + (pbuf ^ 1) * ASLOT + ((lane & 31) * 4 + wave) * 4, alpha);
         }
         if (i + 1 < nst) {
           l_run = l_run * alpha + lsum;
           m_run = m_use;
         }
+        if (stamped) {  // the next iteration starts with this wait anyway
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (i == kStampIter) {
+            stamp_store(5, st_begin);
+            stamp_store(6, st_pass1);
+            stamp_store(7, st_pass2);
+          } else {
+            stamp_store(8, st_begin);
+          }
+        }
       };
       // the other waves: their share of PV(i) and of the copies
       auto pv_iteration = [&]() __attribute__((always_inline)) {
         f32x16 s;
-        pass(std::false_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
-             std::integral_constant<int, PV_START>{}, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{},
-             kst_v, kst_r, vst, pst, s, pass1_hook(std::integral_constant<int, PV_SPLIT + PV_START>{}));
-        pass(std::false_type{}, std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, 2 * SPC>{},
-             std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{},
-             kst_v, kst_r, vst, pst, s, [](auto) {});
+        pass(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{},
+             std::integral_constant<int, PV_SPLIT>{}, std::integral_constant<int, PV_START>{},
+             std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s,
+             pass1_hook(std::integral_constant<int, PV_SPLIT + PV_START>{}));
+        pass(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, PV_SPLIT>{},
+             std::integral_constant<int, 2 * SPC>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{},
+             std::integral_constant<int, 0>{}, kst_v, kst_r, vst, pst, s, [](auto) {});
       };
       if constexpr (NHB == NW) {
         owner_iteration();
@@ -1407,6 +1494,7 @@ void mla_partial_kernel(PartialArgs a) {
     // entry no iteration reads, and the tail then never starts from the
     // initial accumulators (which would have to be kept live across the
     // first loop).
+    if (b == b_first) phase_stamp(2);
     int i = -1;
     for (; i < 0 || i + kStages - 1 < nst; ++i) iteration(i, std::true_type{});
     for (; i < nst; ++i) iteration(i, std::false_type{});
@@ -1414,6 +1502,7 @@ void mla_partial_kernel(PartialArgs a) {
     // finalize reuses them
     wait_vmcnt<0>();
     lds_barrier();
+    if (b == b_first) phase_stamp(3);
 
     // ---- finalize: out = acc / l, lse2 = m + log2(l) -------------------------
     {
@@ -1486,6 +1575,7 @@ void mla_partial_kernel(PartialArgs a) {
       }
     }
 
+    if (b == b_first) phase_stamp(4);
     if (a.fused && !seg.direct) {
       // every wave's write-through partial row and lse stores have
       // completed before the arrival
@@ -1757,6 +1847,19 @@ size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v
   return workspace_bytes(batch, num_heads, head_dim_v, num_splits, num_workers);
 }
 
+int tmla_debug_stamps(void* host, size_t bytes) {
+#if TMLA_STAMPS
+  const size_t n = sizeof(g_stamps) < bytes ? sizeof(g_stamps) : bytes;
+  hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(g_stamps), n, 0, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyFromSymbol(g_stamps)");
+  return TMLA_OK;
+#else
+  (void)host;
+  (void)bytes;
+  return fail(TMLA_ERR_UNSUPPORTED, "phase stamps need a library built with TMLA_STAMPS=1 (build.py --stamps)");
+#endif
+}
+
 int32_t tmla_device_cu_count(int32_t device) {
   int n = 0;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
@@ -1790,6 +1893,8 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
     return fail(TMLA_ERR_INVALID_ARGUMENT, "q, kv and out must be 16-byte aligned");
   if ((q_stride_b | q_stride_h | kv_stride_0 | kv_stride_1 | out_stride_b | out_stride_h) & 7)
     return fail(TMLA_ERR_INVALID_ARGUMENT, "strides must be multiples of 8 elements");
+  if (kv_stride_1 <= 0 || kv_stride_1 > (1 << 25))
+    return fail(TMLA_ERR_UNSUPPORTED, "kv token stride must be in (0, 2^25] elements");
 
   PartialArgs a{};
   a.q = static_cast<const char*>(q);

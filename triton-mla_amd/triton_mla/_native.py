@@ -14,7 +14,10 @@ import threading
 
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtriton_mla_hip.so")
+# TRITON_MLA_LIB selects another build of the library (e.g. the phase-stamp
+# profiling build, libtriton_mla_hip_stamps.so)
+LIB_PATH = os.environ.get("TRITON_MLA_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                            "libtriton_mla_hip.so")
 
 # name -> (restype, argtypes); mirrors include/triton_mla.h
 _i32, _i64, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
@@ -24,6 +27,7 @@ SIGNATURES = {
     "tmla_version": (ctypes.c_int, []),
     "tmla_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "tmla_device_cu_count": (_i32, [_i32]),
+    "tmla_debug_stamps": (ctypes.c_int, [_vp, _sz]),
     "tmla_workspace_zero_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "tmla_mla_decode_fused_is_single": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64, _i32]),
     "tmla_mla_decode_partial": (ctypes.c_int, [
