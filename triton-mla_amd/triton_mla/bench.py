@@ -68,6 +68,8 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
 
     t_compile = None
     if compiled is not None:
+        print(f"# compiling the torch.compile leg for batch {inp.batch}, heads {inp.heads}, "
+              f"max length {int(inp.seqlens.max())}", flush=True)
         ref = run_torch(compiled)
         torch.testing.assert_close(out.float(), ref.float(), atol=2e-2, rtol=2e-2)
         t_compile = time_us(lambda: run_torch(compiled), reps=args.reps, flush=flush, device=device)["median"]
