@@ -218,6 +218,49 @@ int tmla_mla_decode_causal(const void* q, int64_t q_stride_b, int64_t q_stride_h
                            int64_t out_stride_b, int64_t out_stride_h, float* lse, void* workspace,
                            size_t workspace_bytes, int32_t single_launch, void* stream);
 /*
+ * Decode over an fp8 latent cache, no counterpart in the reference (its
+ * README.md:32-33 lists "no FP8 cache" among the limitations). Both stages,
+ * like tmla_mla_decode_causal (q_len = 1: single-token decode), with:
+ *   kv       one byte per element, OCP FP8 E4M3 ("e4m3fn": bias 7, no
+ *            infinities, 0x7f/0xff NaN), same layout as the 16-bit cache with
+ *            strides in elements (= bytes); page_size a multiple of 16 when
+ *            paged; strides multiples of 16.
+ *   kv_scale float32; cache row t of sequence b stands for
+ *            e4m3(byte) * kv_scale[page * scale_stride_0 + (t % page_size) *
+ *            scale_stride_1] (dense: kv_scale[b * scale_stride_0 + t *
+ *            scale_stride_1]): one scale per page (stride_1 = 0), per token,
+ *            or per tensor (both 0). The array must hold every index a page
+ *            id < num_blocks and a row < page_size can form.
+ *   dtype    the element type of q and out (TMLA_BF16 or TMLA_FP16).
+ * The attention is the reference's over the dequantised cache: scores of
+ * the widened (exact) fp8 values times the row's scale, probabilities times
+ * the row's scale rounded to dtype for the value product, float32
+ * accumulation. The workspace is tmla_workspace_bytes(batch, q_len *
+ * num_heads, ...); the partials use tmla_mla_decode_combine's format.
+ */
+int tmla_mla_decode_fp8(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                        int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
+                        const float* kv_scale, int64_t scale_stride_0, int64_t scale_stride_1,
+                        const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols,
+                        const int32_t* seqlens, int32_t batch, int32_t q_len, int32_t num_heads,
+                        int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale,
+                        int32_t num_splits, int32_t num_workers, void* out, int64_t out_stride_b,
+                        int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes,
+                        void* stream);
+/*
+ * Stage 1 of tmla_mla_decode_fp8 alone (q_len = 1); stage 2 is
+ * tmla_mla_decode_combine with the same partition arguments.
+ */
+int tmla_mla_decode_fp8_partial(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                                int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks,
+                                int32_t page_size, const float* kv_scale, int64_t scale_stride_0,
+                                int64_t scale_stride_1, const int32_t* block_table, int64_t bt_stride_b,
+                                int32_t bt_cols, const int32_t* seqlens, int32_t batch,
+                                int32_t num_heads, int32_t head_dim_v, int32_t rope_dim, int32_t dtype,
+                                float softmax_scale, int32_t num_splits, int32_t num_workers, void* out,
+                                int64_t out_stride_b, int64_t out_stride_h, float* lse, void* workspace,
+                                size_t workspace_bytes, void* stream);
+/*
  * Profiling hook, no counterpart in the reference: copies the partial
  * kernel's phase stamps of the last launch into `host` (up to `bytes`):
  * 4096 workers x 9 slots x {100 MHz wall clock, shader clock} uint64 (slot

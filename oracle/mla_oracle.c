@@ -14,6 +14,10 @@
  *   - the stage-1/stage-2 split-and-merge algebra of the fused kernel,
  *     kernel.py:83-86 (split ranges), 119-128 (online softmax + guards),
  *     165-181 (log-sum-exp merge), used to pin split invariance.
+ *   - an fp8 latent cache (no counterpart in the reference, whose README.md
+ *     :32-33 lists "no FP8 cache"): OCP FP8 E4M3 ("e4m3fn") decoding and
+ *     round-to-nearest-even encoding, and mla_decode_ref over the cache
+ *     dequantised as e4m3(byte) * scale[page * s0 + row_in_page * s1].
  *
  * Pins (see tests/test_oracle.py):
  *   gather_kv          bit-exact against torch indexing of the same cache and
@@ -24,6 +28,19 @@
  *                      inputs, token-permutation invariance.
  *   get_num_splits     the 16-row known-answer table in results/bench_h100.csv.
  *   split_merge        equals mla_decode_ref for every split count.
+ *   e4m3 decode        closed forms (0, 1, 448, 2^-9, 2^-6, NaN codes, sign
+ *                      symmetry), monotonicity, and torch.float8_e4m3fn's
+ *                      decoding of all 256 codes.
+ *   e4m3 encode        decode-encode round trip of every code, tie cases
+ *                      (to even mantissa), overflow to NaN above 464, and
+ *                      torch's float32 -> float8_e4m3fn rounding on random
+ *                      values.
+ *   mla_decode_fp8_ref equals mla_decode_ref bit for bit on the same values
+ *                      as a bf16 cache (power-of-two scales keep every
+ *                      dequantised value a bf16 value), a numpy float64
+ *                      softmax over the dequantised cache for arbitrary
+ *                      per-token scales, and per-page == per-token scales
+ *                      that repeat the page's value.
  *
  * Element types: 0 = bfloat16, 1 = float16 (raw 16-bit patterns).
  */
@@ -121,6 +138,62 @@ void oracle_gather_kv(const uint16_t* kv, int64_t kv_s0, int64_t kv_s1, const in
 }
 
 /*
+ * Attention of every head of sequence b over n rows k[t * dqk + c] (float64):
+ *   s = q[b, h] . k^T * scale;  lse = logsumexp(s);  out = softmax(s) . k[:, :dv]
+ * (reference.py:16-31). Writes out (float32, unrounded) and the natural-log
+ * lse of the heads of b. Returns 2 on an allocation failure.
+ */
+static int attend_rows(const double* k, int64_t n, const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t b,
+                       int64_t heads, int64_t dqk, int64_t dv, int dtype, double scale, float* out, float* lse) {
+    int failed = 0;
+#pragma omp parallel
+    {
+        double* s = (double*)malloc((size_t)n * sizeof(double));
+        double* qd = (double*)malloc((size_t)dqk * sizeof(double));
+        double* acc = (double*)malloc((size_t)dv * sizeof(double));
+        if (!s || !qd || !acc) {
+#pragma omp atomic write
+            failed = 1;
+        } else {
+#pragma omp for schedule(dynamic, 1)
+            for (int64_t h = 0; h < heads; ++h) {
+                const uint16_t* qr = q + b * q_sb + h * q_sh;
+                for (int64_t c = 0; c < dqk; ++c) qd[c] = half_bits_to_double(qr[c], dtype);
+                double m = -INFINITY;
+                for (int64_t t = 0; t < n; ++t) {
+                    const double* kr = k + t * dqk;
+                    double dot = 0.0;
+                    for (int64_t c = 0; c < dqk; ++c) dot += qd[c] * kr[c];
+                    s[t] = dot * scale;
+                    if (s[t] > m) m = s[t];
+                }
+                double l = 0.0;
+                for (int64_t c = 0; c < dv; ++c) acc[c] = 0.0;
+                for (int64_t t = 0; t < n; ++t) {
+                    const double p = exp(s[t] - m);
+                    const double* kr = k + t * dqk;
+                    l += p;
+                    for (int64_t c = 0; c < dv; ++c) acc[c] += p * kr[c];
+                }
+                lse[b * heads + h] = (float)(m + log(l));
+                for (int64_t c = 0; c < dv; ++c) out[(b * heads + h) * dv + c] = (float)(acc[c] / l);
+            }
+        }
+        free(s);
+        free(qd);
+        free(acc);
+    }
+    return failed ? 2 : 0;
+}
+
+static void empty_sequence(int64_t b, int64_t heads, int64_t dv, float* out, float* lse) {
+    for (int64_t h = 0; h < heads; ++h) {
+        lse[b * heads + h] = -INFINITY;
+        for (int64_t c = 0; c < dv; ++c) out[(b * heads + h) * dv + c] = 0.0f;
+    }
+}
+
+/*
  * mla_decode_ref (reference.py:16-31), float64 throughout:
  *   s = q[b] . k^T * scale;  lse = logsumexp(s);  out = softmax(s) . k[:, :dv]
  *   n == 0  =>  out = 0, lse = -inf.
@@ -142,10 +215,7 @@ int oracle_mla_decode_ref(const uint16_t* q, int64_t q_sb, int64_t q_sh, const u
     for (int64_t b = 0; b < batch; ++b) {
         const int64_t n = seqlens[b];
         if (n <= 0) {
-            for (int64_t h = 0; h < heads; ++h) {
-                lse[b * heads + h] = -INFINITY;
-                for (int64_t c = 0; c < dv; ++c) out[(b * heads + h) * dv + c] = 0.0f;
-            }
+            empty_sequence(b, heads, dv, out, lse);
             continue;
         }
         double* k = (double*)malloc((size_t)(n * dqk) * sizeof(double));
@@ -155,46 +225,95 @@ int oracle_mla_decode_ref(const uint16_t* q, int64_t q_sb, int64_t q_sh, const u
             const uint16_t* row = kv + token_offset(b, t, bt, bt_s0, paged, page_size, kv_s0, kv_s1);
             for (int64_t c = 0; c < dqk; ++c) k[t * dqk + c] = half_bits_to_double(row[c], dtype);
         }
-        int failed = 0;
-#pragma omp parallel
-        {
-            double* s = (double*)malloc((size_t)n * sizeof(double));
-            double* qd = (double*)malloc((size_t)dqk * sizeof(double));
-            double* acc = (double*)malloc((size_t)dv * sizeof(double));
-            if (!s || !qd || !acc) {
-#pragma omp atomic write
-                failed = 1;
-            } else {
-#pragma omp for schedule(dynamic, 1)
-                for (int64_t h = 0; h < heads; ++h) {
-                    const uint16_t* qr = q + b * q_sb + h * q_sh;
-                    for (int64_t c = 0; c < dqk; ++c) qd[c] = half_bits_to_double(qr[c], dtype);
-                    double m = -INFINITY;
-                    for (int64_t t = 0; t < n; ++t) {
-                        const double* kr = k + t * dqk;
-                        double dot = 0.0;
-                        for (int64_t c = 0; c < dqk; ++c) dot += qd[c] * kr[c];
-                        s[t] = dot * scale;
-                        if (s[t] > m) m = s[t];
-                    }
-                    double l = 0.0;
-                    for (int64_t c = 0; c < dv; ++c) acc[c] = 0.0;
-                    for (int64_t t = 0; t < n; ++t) {
-                        const double p = exp(s[t] - m);
-                        const double* kr = k + t * dqk;
-                        l += p;
-                        for (int64_t c = 0; c < dv; ++c) acc[c] += p * kr[c];
-                    }
-                    lse[b * heads + h] = (float)(m + log(l));
-                    for (int64_t c = 0; c < dv; ++c) out[(b * heads + h) * dv + c] = (float)(acc[c] / l);
-                }
-            }
-            free(s);
-            free(qd);
-            free(acc);
-        }
+        const int rc = attend_rows(k, n, q, q_sb, q_sh, b, heads, dqk, dv, dtype, scale, out, lse);
         free(k);
-        if (failed) return 2;
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+/*
+ * OCP FP8 E4M3 (the "e4m3fn" encoding: bias 7, no infinities, NaN =
+ * S.1111.111) to double, exact: exponent field 0 holds the subnormals
+ * m * 2^-9, field e > 0 the normals (1 + m/8) * 2^(e-7).
+ */
+double oracle_e4m3_to_double(uint8_t code) {
+    const int sign = code >> 7, e = (code >> 3) & 15, m = code & 7;
+    if (e == 15 && m == 7) return NAN;
+    const double v = e == 0 ? ldexp((double)m, -9) : ldexp((double)(8 + m), e - 10);
+    return sign ? -v : v;
+}
+
+/*
+ * Nearest E4M3 code to x, ties to the even code (mantissa bit 0 clear).
+ * Magnitudes above the midpoint 464 between the largest finite value (448)
+ * and the next step (480, which is the NaN pattern) give NaN, as does NaN;
+ * the sign of zero is kept. Brute force over the 127 finite magnitudes.
+ */
+uint8_t oracle_double_to_e4m3(double x) {
+    if (isnan(x)) return 0x7f;
+    const uint8_t sign = signbit(x) ? 0x80 : 0x00;
+    const double a = fabs(x);
+    if (a > 464.0) return (uint8_t)(sign | 0x7f);
+    int best = 0;
+    double best_d = INFINITY;
+    for (int c = 0; c < 127; ++c) {
+        const double d = fabs(oracle_e4m3_to_double((uint8_t)c) - a);
+        if (d < best_d || (d == best_d && (c & 1) == 0)) {
+            best_d = d;
+            best = c;
+        }
+    }
+    return (uint8_t)(sign | best);
+}
+
+void oracle_e4m3_encode(const double* in, uint8_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = oracle_double_to_e4m3(in[i]);
+}
+
+/*
+ * mla_decode_ref over an fp8 cache: kv8 holds E4M3 codes, [num_blocks,
+ * page_size, dqk] with element strides (kv_s0, kv_s1, 1) when paged, else
+ * [batch, capacity, dqk]; row t of sequence b is dequantised as
+ * e4m3(code) * kv_scale[page * sc_s0 + (t % page_size) * sc_s1] (dense:
+ * kv_scale[b * sc_s0 + t * sc_s1]). q (16-bit, dtype) and the outputs are as
+ * for oracle_mla_decode_ref.
+ */
+int oracle_mla_decode_fp8_ref(const uint16_t* q, int64_t q_sb, int64_t q_sh, const uint8_t* kv8, int64_t kv_s0,
+                              int64_t kv_s1, const float* kv_scale, int64_t sc_s0, int64_t sc_s1, const int32_t* bt,
+                              int64_t bt_s0, int paged, int64_t page_size, const int32_t* seqlens, int64_t batch,
+                              int64_t heads, int64_t dqk, int64_t dv, int dtype, double scale, int nthreads,
+                              float* out, float* lse) {
+    if (dv > dqk || dqk <= 0 || heads < 0 || batch < 0) return 1;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+    (void)nthreads;
+#endif
+    double table[256];
+    for (int c = 0; c < 256; ++c) table[c] = oracle_e4m3_to_double((uint8_t)c);
+    for (int64_t b = 0; b < batch; ++b) {
+        const int64_t n = seqlens[b];
+        if (n <= 0) {
+            empty_sequence(b, heads, dv, out, lse);
+            continue;
+        }
+        double* k = (double*)malloc((size_t)(n * dqk) * sizeof(double));
+        if (!k) return 2;
+#pragma omp parallel for schedule(static)
+        for (int64_t t = 0; t < n; ++t) {
+            int64_t sidx;
+            if (paged)
+                sidx = (int64_t)bt[b * bt_s0 + t / page_size] * sc_s0 + (t % page_size) * sc_s1;
+            else
+                sidx = b * sc_s0 + t * sc_s1;
+            const double sc = (double)kv_scale[sidx];
+            const uint8_t* row = kv8 + token_offset(b, t, bt, bt_s0, paged, page_size, kv_s0, kv_s1);
+            for (int64_t c = 0; c < dqk; ++c) k[t * dqk + c] = table[row[c]] * sc;
+        }
+        const int rc = attend_rows(k, n, q, q_sb, q_sh, b, heads, dqk, dv, dtype, scale, out, lse);
+        free(k);
+        if (rc) return rc;
     }
     return 0;
 }

@@ -12,6 +12,10 @@ Contents
   kernel's split/merge algebra (kernel.py:83-86, 119-128, 165-181));
 * ``mla_decode_ref_causal``: multi-token causal decode built on the
   single-token oracle (an extension; no reference counterpart);
+* an fp8 latent cache (no reference counterpart; its README.md:32-33 lists
+  "no FP8 cache"): ``e4m3_to_float`` / ``float_to_e4m3`` (OCP E4M3,
+  round to nearest even) and ``mla_decode_fp8_ref`` (the single-token or
+  causal oracle over the dequantised cache);
 * a numpy float64 restatement of the ``MLA`` layer (src/triton_mla/model.py):
   RMSNorm (model.py:34-41), rotate-half RoPE (model.py:44-50), projections
   (model.py:74-82), cache append (model.py:84-94), ``W_UK``/``W_UV`` split
@@ -70,6 +74,13 @@ def lib():
         L.oracle_float_to_half_bits.restype = ctypes.c_uint16
         L.oracle_half_to_double.argtypes = [ctypes.c_uint16, i32]
         L.oracle_half_to_double.restype = f64
+        L.oracle_e4m3_to_double.argtypes = [ctypes.c_uint8]
+        L.oracle_e4m3_to_double.restype = f64
+        L.oracle_e4m3_encode.argtypes = [vp, vp, i64]
+        L.oracle_e4m3_encode.restype = None
+        L.oracle_mla_decode_fp8_ref.argtypes = [vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64, i32, i64,
+                                                vp, i64, i64, i64, i64, i32, f64, i32, vp, vp]
+        L.oracle_mla_decode_fp8_ref.restype = i32
         _lib = L
     return _lib
 
@@ -166,6 +177,80 @@ def mla_decode_ref_causal(q, kv_cache, cache_seqlens, block_table=None, head_dim
                               softmax_scale, dtype, nthreads)
         out[:, t] = o
         lse[:, t] = l
+    return out, lse
+
+
+# ----------------------------------------------------------------------------
+# fp8 (OCP E4M3) latent cache
+# ----------------------------------------------------------------------------
+
+def e4m3_to_float(codes: np.ndarray) -> np.ndarray:
+    """Exact float64 values of E4M3 codes (uint8)."""
+    table = np.array([lib().oracle_e4m3_to_double(c) for c in range(256)], dtype=np.float64)
+    return table[np.asarray(codes, dtype=np.uint8)]
+
+
+def float_to_e4m3(x: np.ndarray) -> np.ndarray:
+    """Nearest E4M3 codes (ties to even; above 464 in magnitude: NaN)."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    out = np.empty(x.shape, dtype=np.uint8)
+    lib().oracle_e4m3_encode(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def mla_decode_fp8_ref(q, kv8, kv_scale, cache_seqlens, block_table=None, head_dim_v=512,
+                       softmax_scale=None, dtype="bf16", scale_strides=None, nthreads=0):
+    """mla_decode_ref over an fp8 cache, float64.
+
+    kv8: uint8 E4M3 codes, [num_blocks, page_size, D] (paged) or [batch,
+    capacity, D] (dense). kv_scale: float32 array; row t of sequence b is
+    dequantised as e4m3(code) * kv_scale.flat[page * s0 + (t % page_size) * s1]
+    (dense: b * s0 + t * s1) with (s0, s1) = scale_strides, by default the
+    array's own element strides (per page: shape [num_blocks]; per token:
+    [num_blocks, page_size]; one scale: any one-element array -> (0, 0)).
+    q is [B, H, D] (single token) or [B, T, H, D] (causal, as
+    mla_decode_ref_causal). Returns ``(out float32 unrounded, lse float32)``.
+    """
+    q = _u16(q)
+    if q.ndim == 4:
+        B, T, H, D = q.shape
+        seqlens = np.asarray(cache_seqlens, dtype=np.int64)
+        out = np.empty((B, T, H, head_dim_v), dtype=np.float32)
+        lse = np.empty((B, T, H), dtype=np.float32)
+        for t in range(T):
+            n_t = np.maximum(seqlens - (T - 1 - t), 0).astype(np.int32)
+            o, l = mla_decode_fp8_ref(np.ascontiguousarray(q[:, t]), kv8, kv_scale, n_t, block_table, head_dim_v,
+                                      softmax_scale, dtype, scale_strides, nthreads)
+            out[:, t] = o
+            lse[:, t] = l
+        return out, lse
+    q = np.ascontiguousarray(q)
+    B, H, dqk = q.shape
+    if softmax_scale is None:
+        softmax_scale = dqk ** -0.5
+    kv8 = np.ascontiguousarray(kv8, dtype=np.uint8)
+    assert kv8.shape[-1] == dqk
+    sc = np.ascontiguousarray(kv_scale, dtype=np.float32)
+    if scale_strides is None:
+        if sc.size == 1:
+            scale_strides = (0, 0)
+        else:
+            st = [s // 4 for s in sc.strides] + [0, 0]
+            scale_strides = (st[0], st[1])
+    seqlens = np.ascontiguousarray(cache_seqlens, dtype=np.int32)
+    if block_table is None:
+        bt, bt_s0, paged, page_size = None, 0, 0, 1
+    else:
+        bt = np.ascontiguousarray(block_table, dtype=np.int32)
+        bt_s0, paged, page_size = bt.shape[1], 1, kv8.shape[1]
+    out = np.empty((B, H, head_dim_v), dtype=np.float32)
+    lse = np.empty((B, H), dtype=np.float32)
+    rc = lib().oracle_mla_decode_fp8_ref(
+        _ptr(q), H * dqk, dqk, _ptr(kv8), kv8.shape[1] * dqk, dqk, _ptr(sc), int(scale_strides[0]),
+        int(scale_strides[1]), _ptr(bt) if bt is not None else None, bt_s0, paged, page_size, _ptr(seqlens),
+        B, H, dqk, head_dim_v, _DTYPE_CODE[dtype], float(softmax_scale), int(nthreads), _ptr(out), _ptr(lse))
+    if rc != 0:
+        raise RuntimeError(f"oracle_mla_decode_fp8_ref failed ({rc})")
     return out, lse
 
 

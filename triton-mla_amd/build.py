@@ -23,7 +23,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "triton_mla", "libtriton_mla_hip.so")
 LIB_STAMPS = os.path.join(HERE, "triton_mla", "libtriton_mla_hip_stamps.so")
-SOURCES = ["mla_decode.hip", "mla_layer.hip"]
+SOURCES = ["mla_decode.hip", "mla_decode_fp8.hip", "mla_layer.hip"]
 ARCH = os.environ.get("TRITON_MLA_ARCH", "gfx950")
 
 

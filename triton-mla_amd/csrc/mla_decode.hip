@@ -37,11 +37,11 @@
 #include <utility>
 
 #include "cdna.h"
+#include "decode_common.h"
 #include "triton_mla.h"
 
 namespace tmla {
 
-constexpr int kTileTokens = 64;     // planning unit (one page at page_size 64)
 constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 // Schedule of the partial kernel's tile loop (build-time knobs): LDS operand
 // reads issued this many MFMA steps ahead of their use; PV MFMAs beside the
@@ -83,45 +83,6 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 #endif
 constexpr int kStages = 4;          // LDS ring depth (3 sub-tiles in flight)
 constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
-constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (p <= 2^8)
-constexpr float kNoMax = -__FLT_MAX__;  // running max of a head that has seen no token
-constexpr float kLn2 = 0.6931471805599453f;
-constexpr float kLog2e = 1.4426950408889634f;
-
-struct PartialArgs {
-  const char* q;           // element pointer (bytes)
-  int64_t q_sb, q_sh;      // element strides
-  const char* kv;
-  int64_t kv_s0, kv_s1;    // byte strides: block (dense: batch), token
-  int64_t num_blocks;
-  int32_t max_page;               // min(num_blocks - 1, INT32_MAX): page ids are clamped to it
-  int32_t page_size, page_shift;  // page_shift = log2(page_size) or -1
-  const int32_t* bt;
-  int64_t bt_sb;
-  int32_t bt_cols;
-  const int32_t* seqlens;
-  int32_t batch, num_heads;
-  // Multi-token queries: head index v = t * heads_per_token + h for query
-  // token t < q_len, which sees the first seqlen - (q_len - 1 - t) tokens
-  // (q_len = 1: single-token decode, every head sees seqlen tokens).
-  int32_t q_len, heads_per_token;
-  float qk_scale_log2;
-  int32_t num_splits, num_workers;
-  int32_t xcds;            // workgroups are dealt round-robin over this many L2 domains
-  char* out;
-  int64_t out_sb, out_sh;  // element strides
-  float* lse;
-  short* mid_o;            // [slots, H, DV] normalised partials, input dtype
-  float* mid_lse;          // [slots, H], base-2
-  // In-kernel merge (fused): the workers of a split sequence each merge one
-  // share of its heads once all of them have stored their partials.
-  int32_t fused;
-  int32_t spin_limit;      // polls before a waiting worker hands its share over
-  int32_t* m_count;        // [batch, head blocks] partials stored
-  int32_t* m_done;         // [batch, head blocks] shares merged
-  int32_t* m_flag;         // [slots, head blocks] 0 owner merges, 1 handed over, 2 taken over
-  int32_t mid_o_bytes;     // bytes of the partial rows (< 2^31 when fused)
-};
 
 struct CombineArgs {
   const int32_t* seqlens;
@@ -178,28 +139,6 @@ __device__ __forceinline__ void stamp_store(int slot, StampRec r) {
 }
 __device__ __forceinline__ void phase_stamp(int slot) { stamp_store(slot, stamp_now()); }
 
-__device__ __forceinline__ int tiles_of(int n) { return n > 0 ? (n + kTileTokens - 1) / kTileTokens : 0; }
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
-
-// The lane id through an instruction the compiler cannot look through:
-// offsets derived from it are recomputed where they are needed instead of
-// being kept live across the whole kernel (where they would be spilled to
-// scratch and reloaded, one memory round trip each, at start-up and in the
-// finalize).
-__device__ __forceinline__ int lane_id_fresh() {
-  int v;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(v));
-  return v;
-}
-
-// Tokens at the end of the sequence that query head `head` does not see:
-// q_len - 1 - t for the head's query token t (0 for single-token decode).
-__device__ __forceinline__ int causal_lag(const PartialArgs& a, int head) {
-  return a.q_len <= 1 ? 0 : a.q_len - 1 - min(head, a.num_heads - 1) / a.heads_per_token;
-}
-
 // Register-class pins: an empty asm that requires its operand in VGPRs /
 // AGPRs at that point. They keep the PV accumulators in AGPRs and the S tile
 // in VGPRs instead of letting the allocator shuttle blocks between files.
@@ -209,13 +148,6 @@ __device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x))
 // of the compiler rejects GPU register constraints inside a kernel body.)
 __device__ __forceinline__ void pin_f1(float& a) { asm volatile("" : "+v"(a)); }
 __device__ __forceinline__ void pin_i1(int& a) { asm volatile("" : "+v"(a)); }
-// A uniform value the compiler must treat as new at this point: divisions by
-// it are not hoisted out of the enclosing loop (their reciprocal would occupy
-// a VGPR for the whole loop).
-__device__ __forceinline__ int fresh_s(int x) {
-  asm volatile("" : "+s"(x));
-  return x;
-}
 __device__ __forceinline__ void pin_f2(float& a, float& b) { asm volatile("" : "+v"(a), "+v"(b)); }
 __device__ __forceinline__ void pin_f3(float& a, float& b, float& c) { asm volatile("" : "+v"(a), "+v"(b), "+v"(c)); }
 __device__ __forceinline__ void pin_f4(f32x4& x) { asm volatile("" : "+v"(x)); }
@@ -299,21 +231,6 @@ constexpr int pass_reads(int t) {
   return n;
 }
 
-// Scalar load of one int (uniform address) with no wait; s_wait_i32 waits
-// for every outstanding LDS/scalar operation and ties the value to that point.
-// Issued only where no LDS read that a later lgkmcnt count relies on is
-// older than it, so the out-of-order scalar return cannot satisfy such a wait
-// early.
-__device__ __forceinline__ int s_load_i32(const int32_t* p) {
-  int r;
-  asm volatile("s_load_dword %0, %1, 0x0" : "=s"(r) : "s"(p));
-  return r;
-}
-__device__ __forceinline__ int s_wait_i32(int v) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v));
-  return v;
-}
-
 // S^T accumulation in VGPRs (the PV accumulators own every AGPR). After the
 // chain, mfma_vgpr_fence waits out the MFMA result latency before any VALU
 // instruction reads the accumulator.
@@ -356,19 +273,6 @@ __device__ __forceinline__ void pack_probs_in_place(f32x16& p) {
 __device__ __forceinline__ i16x8 packed_half(const f32x16& p, int h) {
   const f32x4 v = h == 0 ? f32x4{p[0], p[1], p[2], p[3]} : f32x4{p[4], p[5], p[6], p[7]};
   return __builtin_bit_cast(i16x8, v);
-}
-
-// 16-byte store written through to memory (sc0 sc1: system-scope write-
-// through), so a kernel that ends with many such stores leaves no dirty L2
-// lines for the end-of-kernel write-back. The s_nop supplies the wait state
-// the hardware needs before a VALU instruction may overwrite the data VGPRs
-// of a store wider than 64 bits: the compiler inserts it for the stores it
-// generates, but cannot see into this asm.
-__device__ __forceinline__ void store_through(i16x8* p, i16x8 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ void store_through_f32(float* p, float v) {
-  asm volatile("global_store_dword %0, %1, off sc0 sc1" : : "v"(p), "v"(v) : "memory");
 }
 
 // ---------------------------------------------------------------------------
@@ -680,19 +584,6 @@ __device__ __forceinline__ int64_t row_offset(const PartialArgs& a, int b, int t
   return (int64_t)page_id * a.kv_s0 + (int64_t)in_page * a.kv_s1;
 }
 
-// POW2: the page size is known to be a power of two (page_shift >= 0)
-template <bool POW2 = false>
-__device__ __forceinline__ int page_slot_of(const PartialArgs& a, int t) {
-  const int s = (POW2 || a.page_shift >= 0) ? (t >> a.page_shift) : (t / a.page_size);
-  return min(s, a.bt_cols - 1);
-}
-
-__device__ __forceinline__ int load_page(const PartialArgs& a, int b, int slot) {
-  int p = a.bt[(int64_t)b * a.bt_sb + slot];
-  p = p < 0 ? 0 : p;
-  return min(p, a.max_page);
-}
-
 // Segment of a worker: tiles [t0, t1) of sequence b, result goes to `slot`
 // (a partial) or straight to out/lse when `direct`.
 struct Segment {
@@ -764,14 +655,8 @@ void mla_partial_kernel(PartialArgs a) {
   phase_stamp(0);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar LDS bases
-  // Logical worker index: consecutive workers (the pieces of one sequence,
-  // which share its Q rows and write neighbouring partial slots) are placed
-  // on the same XCD, since the dispatcher deals workgroups round-robin over
-  // the XCDs and each XCD has its own L2.
   const int nwg = gridDim.x;
-  const int worker = (a.xcds > 1 && nwg % a.xcds == 0)
-                         ? (int)(blockIdx.x % a.xcds) * (nwg / a.xcds) + (int)(blockIdx.x / a.xcds)
-                         : (int)blockIdx.x;
+  const int worker = worker_index(a);
   const bool s_owner = NHB == 4 || wave < NHB;  // runs S and the softmax of head block `wave`
   const int head_base = blockIdx.y * (kHeadsPerWave * NHB) + wave * kHeadsPerWave;
   // the wave's first head has its earliest query token: the most tokens unseen
@@ -784,98 +669,12 @@ void mla_partial_kernel(PartialArgs a) {
   if (a.fused && tid == 0) s_pend[0][0] = s_pend[1][0] = -1;
 
   // ---- work range -------------------------------------------------------
-  int b_first, tile_lo, tile_hi, off_first, n_first, chunk = 0;
-  bool snapped = false;  // balanced: one piece of one sequence per worker
-  if (a.num_splits > 0) {
-    const int S = a.num_splits;
-    const int b = worker / S, s = worker - b * S;
-    n_first = a.seqlens[b];
-    const int nt = tiles_of(n_first);
-    const int spt = (nt + S - 1) / S;
-    tile_lo = s * spt;
-    tile_hi = min(tile_lo + spt, nt);
-    b_first = b;
-    off_first = 0;
-  } else {
-    // Balanced: the T tiles of all sequences (in order) are cut into
-    // num_workers ranges of c = cdiv(T, num_workers) tiles. Every wave
-    // computes the partition on its own (registers and cross-lane moves
-    // only, no LDS or barrier): lane l sums the tile counts of sequences
-    // [l * per, (l + 1) * per), a wave-wide inclusive scan gives each lane
-    // the tile offset where its sequences end.
-    const int lane0 = lane_id_fresh();
-    const int per = (a.batch + 63) >> 6;
-    const int lo_b = min(lane0 * per, a.batch), hi_b = min(lo_b + per, a.batch);
-    const int len0 = lo_b < hi_b ? a.seqlens[lo_b] : 0;
-    int sum = tiles_of(len0);
-    for (int b = lo_b + 1; b < hi_b; ++b) sum += tiles_of(a.seqlens[b]);
-    int incl = sum;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int v = __shfl_up(incl, d);
-      if (lane0 >= d) incl += v;
-    }
-    const int total = __builtin_amdgcn_readlane(incl, 63);
-    chunk = (total + a.num_workers - 1) / a.num_workers;
-    // Snapped ranges: when every sequence cut into pieces of at most c tiles
-    // gives no more pieces than workers, worker w takes piece w instead (the
-    // pieces of each sequence in order, piece j = tiles [j c, (j + 1) c)).
-    // The longest range is still c tiles, and no worker pays a second
-    // start-up and finalize for a range that straddles two sequences.
-    int pcs = 0, pinc = 0;
-    if (chunk > 0) {
-      pcs = (tiles_of(len0) + chunk - 1) / chunk;  // len0 = 0 for a lane without sequences
-      for (int b = lo_b + 1; b < hi_b; ++b) pcs += (tiles_of(a.seqlens[b]) + chunk - 1) / chunk;
-      pinc = pcs;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int v = __shfl_up(pinc, d);
-        if (lane0 >= d) pinc += v;
-      }
-      snapped = __builtin_amdgcn_readlane(pinc, 63) <= a.num_workers;
-    }
-    const int lo = worker * chunk;
-    if (snapped && worker < __builtin_amdgcn_readlane(pinc, 63)) {
-      // the one lane whose sequences hold piece `worker` finds which of them
-      int poff = pinc - pcs, off = incl - sum, fb = lo_b, flen = len0;
-      for (int b = lo_b; b < hi_b; ++b) {
-        const int len = b == lo_b ? len0 : a.seqlens[b];
-        const int nt = tiles_of(len);
-        const int np = (nt + chunk - 1) / chunk;
-        fb = b;
-        flen = len;
-        if (worker < poff + np) break;
-        poff += np;
-        off += nt;
-      }
-      const int src = __builtin_ctzll(__ballot(pcs > 0 && pinc - pcs <= worker && worker < pinc));
-      b_first = __builtin_amdgcn_readlane(fb, src);
-      off_first = __builtin_amdgcn_readlane(off, src);
-      n_first = __builtin_amdgcn_readlane(flen, src);
-      tile_lo = (worker - __builtin_amdgcn_readlane(poff, src)) * chunk;  // local to b_first
-      tile_hi = min(tile_lo + chunk, tiles_of(n_first));
-    } else if (snapped || lo >= total) {  // wave-uniform, and the same in every wave
-      if (!a.fused) return;  // (the fused tail still clears empty sequences)
-      b_first = off_first = n_first = tile_lo = tile_hi = 0;
-    } else {
-      // the one lane whose sequences hold tile lo finds which of them it is
-      int off = incl - sum, fb = lo_b, flen = len0;
-      for (int b = lo_b; b < hi_b; ++b) {
-        const int len = b == lo_b ? len0 : a.seqlens[b];
-        const int nt = tiles_of(len);
-        fb = b;
-        flen = len;
-        if (lo < off + nt) break;
-        off += nt;
-      }
-      const int src = __builtin_ctzll(__ballot(sum > 0 && incl - sum <= lo && lo < incl));
-      b_first = __builtin_amdgcn_readlane(fb, src);
-      off_first = __builtin_amdgcn_readlane(off, src);
-      n_first = __builtin_amdgcn_readlane(flen, src);
-      tile_lo = lo - off_first;                      // local to b_first
-      tile_hi = min(lo + chunk, total) - off_first;  // may run past b_first
-    }
+  WorkRange wr;
+  if (!work_range(a, worker, wr)) {
+    if (!a.fused) return;  // (the fused tail still clears empty sequences)
   }
+  const int b_first = wr.b_first, tile_lo = wr.tile_lo, tile_hi = wr.tile_hi;
+  const int off_first = wr.off_first, n_first = wr.n_first;
   if (a.fused) {
     // empty sequences worker, worker + nwg, ...: out = 0, lse = -inf
     // (kernel.py:126-128, 178-181); the first length was requested at entry
@@ -949,35 +748,18 @@ void mla_partial_kernel(PartialArgs a) {
     seg.b = b;
     seg.t0 = t_start;
     seg.t1 = t_end;
-    if (a.num_splits > 0) {
-      const int S = a.num_splits;
-      const int spt = (nt_b + S - 1) / S;
-      const int count = (nt_b + spt - 1) / spt;
-      seg.slot = b * S + t_start / spt;
-      seg.direct = count == 1;
+    {
+      const SegmentSlot ss = segment_slot(a, wr, worker, b, t_start, nt_b, seg_global_off);
+      seg.slot = ss.slot;
+      seg.direct = ss.direct;
       // fused merge record: b, this worker's index among b's workers, their
       // count, b's first slot
       if (a.fused && !seg.direct && wave == 0 && lane == 0) {
         int* r = s_pend[b == b_first ? 0 : 1];
         r[0] = b;
-        r[1] = t_start / spt;
-        r[2] = count;
-        r[3] = b * S;
-      }
-    } else {
-      const int ch = fresh_s(chunk);
-      // the workers of b: g1..g2 (straddling ranges) or g1 = worker - j ..
-      // g1 + pieces - 1 (snapped: this is piece j = t_start / c of b)
-      const int g1 = snapped ? worker - t_start / ch : seg_global_off / ch;
-      const int g2 = snapped ? g1 + (nt_b + ch - 1) / ch - 1 : (seg_global_off + nt_b - 1) / ch;
-      seg.slot = worker + b;
-      seg.direct = g1 == g2;
-      if (a.fused && !seg.direct && wave == 0 && lane == 0) {
-        int* r = s_pend[b == b_first ? 0 : 1];
-        r[0] = b;
-        r[1] = worker - g1;
-        r[2] = g2 - g1 + 1;
-        r[3] = g1 + b;
+        r[1] = ss.index;
+        r[2] = ss.count;
+        r[3] = ss.first_slot;
       }
     }
 
@@ -1768,22 +1550,27 @@ struct LaunchPlan {
   bool fused;
 };
 
+// Workgroups along the workers: all of them for uniform splits; for the
+// balanced partition no more than the 64-token tiles the call can hold
+// (block-table width or dense capacity: capacity_tokens per sequence), since
+// workers past them never get a range.
+int worker_grid(int32_t batch, int32_t num_splits, int32_t num_workers, int64_t capacity_tokens) {
+  const int workers = num_splits > 0 ? batch * num_splits : num_workers;
+  const int64_t tile_bound = (int64_t)batch * ((capacity_tokens + kTileTokens - 1) / kTileTokens);
+  return num_splits > 0 ? workers : (int)(tile_bound < workers ? (tile_bound > 0 ? tile_bound : 1) : workers);
+}
+
 // capacity_tokens: tokens the block table (or dense cache) can hold per
 // sequence; mode as in decode_launch.
 LaunchPlan plan_launch(int32_t batch, int32_t num_heads, int32_t num_splits, int32_t num_workers,
                        int64_t capacity_tokens, size_t mid_o_bytes, int mode, int cus) {
   LaunchPlan p;
   p.nhb = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
-  const int workers = num_splits > 0 ? batch * num_splits : num_workers;
-  // Upper bound of the 64-token tiles the call can hold (block-table width or
-  // dense capacity): balanced workers past it never get a range, so the grid
-  // stops there, and when the busy workgroups would leave compute units idle,
-  // fewer heads per workgroup (more, shorter workgroups: less Q to load, less
-  // MFMA work per sub-tile, smaller partial rows) use them. The single-launch
-  // merge keeps the head blocks its counters are laid out for.
-  const int64_t tile_bound = (int64_t)batch * ((capacity_tokens + kTileTokens - 1) / kTileTokens);
-  const int grid_x =
-      num_splits > 0 ? workers : (int)(tile_bound < workers ? (tile_bound > 0 ? tile_bound : 1) : workers);
+  // When the busy workgroups would leave compute units idle, fewer heads per
+  // workgroup (more, shorter workgroups: less Q to load, less MFMA work per
+  // sub-tile, smaller partial rows) use them. The single-launch merge keeps
+  // the head blocks its counters are laid out for.
+  const int grid_x = worker_grid(batch, num_splits, num_workers, capacity_tokens);
   if (mode != 1) {
     while (p.nhb > 1 && (int64_t)grid_x * ((num_heads + 16 * p.nhb - 1) / (16 * p.nhb)) <= cus) p.nhb /= 2;
   }
@@ -1797,6 +1584,13 @@ LaunchPlan plan_launch(int32_t batch, int32_t num_heads, int32_t num_splits, int
 
 struct Common {
   int32_t batch, heads, dv, dr, dtype, splits, workers;
+};
+
+// Scales of an fp8 cache: element strides per page (dense: per sequence)
+// and per row.
+struct Fp8Scales {
+  const float* scale;
+  int64_t s0, s1;
 };
 
 int check_common(const Common& c, const void* workspace, size_t ws_bytes) {
@@ -1840,7 +1634,7 @@ extern "C" {
 
 const char* tmla_last_error(void) { return g_err; }
 
-int tmla_version(void) { return 200; }
+int tmla_version(void) { return 300; }
 
 size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v, int32_t num_splits,
                             int32_t num_workers) {
@@ -1878,7 +1672,7 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
                   int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale, int32_t num_splits,
                   int32_t num_workers, void* out, int64_t out_stride_b, int64_t out_stride_h, float* lse,
                   void* workspace, size_t workspace_bytes_, void* stream, int mode, int32_t q_len = 1,
-                  int32_t spin_limit = -1) {
+                  int32_t spin_limit = -1, const Fp8Scales* f8 = nullptr) {
   const Common c{batch, num_heads, head_dim_v, rope_dim, dtype, num_splits, num_workers};
   int rc = check_common(c, workspace, workspace_bytes_);
   if (rc != TMLA_OK) return rc;
@@ -1893,6 +1687,14 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
     return fail(TMLA_ERR_INVALID_ARGUMENT, "q, kv and out must be 16-byte aligned");
   if ((q_stride_b | q_stride_h | kv_stride_0 | kv_stride_1 | out_stride_b | out_stride_h) & 7)
     return fail(TMLA_ERR_INVALID_ARGUMENT, "strides must be multiples of 8 elements");
+  if (f8) {
+    if ((kv_stride_0 | kv_stride_1) & 15)
+      return fail(TMLA_ERR_INVALID_ARGUMENT, "fp8 cache strides must be multiples of 16 elements");
+    if (paged && page_size % 16 != 0)
+      return fail(TMLA_ERR_UNSUPPORTED, "fp8 cache pages must hold a multiple of 16 tokens");
+    if (!f8->scale || ((uintptr_t)f8->scale & 3))
+      return fail(TMLA_ERR_INVALID_ARGUMENT, "kv_scale must be a 4-byte aligned float32 pointer");
+  }
   if (kv_stride_1 <= 0 || kv_stride_1 > (1 << 25))
     return fail(TMLA_ERR_UNSUPPORTED, "kv token stride must be in (0, 2^25] elements");
 
@@ -1901,8 +1703,9 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   a.q_sb = q_stride_b;
   a.q_sh = q_stride_h;
   a.kv = static_cast<const char*>(kv);
-  a.kv_s0 = kv_stride_0 * 2;
-  a.kv_s1 = kv_stride_1 * 2;
+  const int kv_elt = f8 ? 1 : 2;  // bytes per cache element
+  a.kv_s0 = kv_stride_0 * kv_elt;
+  a.kv_s1 = kv_stride_1 * kv_elt;
   a.num_blocks = num_blocks;
   a.max_page = (int32_t)(num_blocks - 1 < INT32_MAX ? num_blocks - 1 : INT32_MAX);
   a.page_size = page_size;
@@ -1944,6 +1747,20 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
 
   const int64_t cap_tokens = paged ? (int64_t)bt_cols * page_size : num_blocks;
   const size_t mid_o_bytes = wl.l - wl.o;  // partial rows, 256-byte aligned
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (f8) {
+    // fp8 cache: groups of 16 heads, always two launches (no in-kernel merge)
+    a.kv_scale = f8->scale;
+    a.sc_s0 = f8->s0;
+    a.sc_s1 = f8->s1;
+    const dim3 grid(worker_grid(batch, num_splits, num_workers, cap_tokens), (num_heads + 15) / 16);
+    hipError_t e = launch_partial_fp8(a, grid, dtype, paged, s);
+    if (e != hipSuccess) return hip_fail(e, "mla_partial_fp8_kernel launch");
+    if (mode != 0)
+      return tmla_mla_decode_combine(seqlens, batch, num_heads, head_dim_v, dtype, num_splits, num_workers, out,
+                                     out_stride_b, out_stride_h, lse, workspace, workspace_bytes_, stream);
+    return TMLA_OK;
+  }
   const LaunchPlan plan =
       plan_launch(batch, num_heads, num_splits, num_workers, cap_tokens, mid_o_bytes, mode, current_cu_count());
   const int nhb = plan.nhb;
@@ -1953,7 +1770,6 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   // one page per 32-token sub-tile (sub-tiles never straddle a page) and a
   // power-of-two page size: page slots and in-page rows by shifts and masks
   const bool uni = paged && (page_size % kSubTokens == 0) && a.page_shift >= 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = dtype == TMLA_BF16 ? launch_partial_dt<TMLA_BF16>(a, grid, nhb, s, paged, uni)
                                     : launch_partial_dt<TMLA_FP16>(a, grid, nhb, s, paged, uni);
   if (e != hipSuccess) return hip_fail(e, "mla_partial_kernel launch");
@@ -2136,6 +1952,37 @@ int tmla_mla_decode_causal(const void* q, int64_t q_stride_b, int64_t q_stride_h
                        bt_stride_b, bt_cols, seqlens, batch, q_len * num_heads, head_dim_v, rope_dim, dtype,
                        softmax_scale, num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace,
                        workspace_bytes_, stream, single_launch ? 1 : 2, q_len);
+}
+
+int tmla_mla_decode_fp8(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv, int64_t kv_stride_0,
+                        int64_t kv_stride_1, int64_t num_blocks, int32_t page_size, const float* kv_scale,
+                        int64_t scale_stride_0, int64_t scale_stride_1, const int32_t* block_table,
+                        int64_t bt_stride_b, int32_t bt_cols, const int32_t* seqlens, int32_t batch, int32_t q_len,
+                        int32_t num_heads, int32_t head_dim_v, int32_t rope_dim, int32_t dtype, float softmax_scale,
+                        int32_t num_splits, int32_t num_workers, void* out, int64_t out_stride_b,
+                        int64_t out_stride_h, float* lse, void* workspace, size_t workspace_bytes_, void* stream) {
+  if (q_len < 1 || num_heads <= 0 || (int64_t)q_len * num_heads > INT32_MAX)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "q_len must be >= 1 and q_len * num_heads must fit int32");
+  const Fp8Scales f8{kv_scale, scale_stride_0, scale_stride_1};
+  return decode_launch(q, q_stride_b, q_stride_h, kv, kv_stride_0, kv_stride_1, num_blocks, page_size, block_table,
+                       bt_stride_b, bt_cols, seqlens, batch, q_len * num_heads, head_dim_v, rope_dim, dtype,
+                       softmax_scale, num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace,
+                       workspace_bytes_, stream, 2, q_len, -1, &f8);
+}
+
+int tmla_mla_decode_fp8_partial(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                                int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
+                                const float* kv_scale, int64_t scale_stride_0, int64_t scale_stride_1,
+                                const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols,
+                                const int32_t* seqlens, int32_t batch, int32_t num_heads, int32_t head_dim_v,
+                                int32_t rope_dim, int32_t dtype, float softmax_scale, int32_t num_splits,
+                                int32_t num_workers, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                                float* lse, void* workspace, size_t workspace_bytes_, void* stream) {
+  const Fp8Scales f8{kv_scale, scale_stride_0, scale_stride_1};
+  return decode_launch(q, q_stride_b, q_stride_h, kv, kv_stride_0, kv_stride_1, num_blocks, page_size, block_table,
+                       bt_stride_b, bt_cols, seqlens, batch, num_heads, head_dim_v, rope_dim, dtype, softmax_scale,
+                       num_splits, num_workers, out, out_stride_b, out_stride_h, lse, workspace, workspace_bytes_,
+                       stream, 0, 1, -1, &f8);
 }
 
 }  // extern "C"

@@ -3,6 +3,7 @@
 Drop-in for the reference package's public API (src/triton_mla/__init__.py:1-14).
 """
 
+from .fp8 import dequantize_kv_fp8, quantize_kv_fp8
 from .kernel import get_num_splits, mla_decode
 from .model import MLA, MLAConfig
 from .reference import mla_decode_ref, mla_decode_torch
@@ -12,8 +13,10 @@ __version__ = "0.1.1"
 __all__ = [
     "MLA",
     "MLAConfig",
+    "dequantize_kv_fp8",
     "get_num_splits",
     "mla_decode",
     "mla_decode_ref",
     "mla_decode_torch",
+    "quantize_kv_fp8",
 ]

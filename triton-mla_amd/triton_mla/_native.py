@@ -47,6 +47,12 @@ SIGNATURES = {
     "tmla_mla_decode_causal": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32,
         _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _i32, _vp]),
+    "tmla_mla_decode_fp8": (ctypes.c_int, [
+        _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
+        _i32, _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "tmla_mla_decode_fp8_partial": (ctypes.c_int, [
+        _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _i32,
+        _i32, _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "tmla_mla_absorb_q": (ctypes.c_int, [
         _vp, _i64, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp, _i64, _i64, _vp]),
     "tmla_mla_absorb_out": (ctypes.c_int, [

@@ -8,7 +8,10 @@ the C ABI in include/triton_mla.h:
   * ``tmla_mla_decode_partial`` -- split-KV partial attention (replaces the
     reference's stage-1 launch, kernel.py:276-302);
   * ``tmla_mla_decode_combine`` -- log-sum-exp merge (replaces the stage-2
-    launch, kernel.py:303-320).
+    launch, kernel.py:303-320);
+  * ``tmla_mla_decode_fp8`` / ``_fp8_partial`` -- the same decode over an
+    fp8 (E4M3) latent cache with per-page, per-token or per-tensor scales
+    (no reference counterpart: its README.md:32-33 lists "no FP8 cache").
 
 Tensors stay on the GPU; there is no CPU or eager fallback. With
 ``num_splits=None`` the token-balanced work partition is computed on the
@@ -22,6 +25,7 @@ import torch
 from . import _native
 
 _DTYPES = (torch.bfloat16, torch.float16)
+_FP8_CACHE = (torch.float8_e4m3fn, torch.uint8)  # E4M3 codes (uint8: the raw bytes)
 _SUPPORTED_DIMS = {(512, 64)}  # (head_dim_v, rope_dim) with compiled kernels
 
 
@@ -64,8 +68,28 @@ def get_num_splits(batch, num_heads, max_seqlen, num_sms, min_tokens_per_split=1
 DEFAULT_SINGLE_LAUNCH = False
 
 
-def _aligned(t: torch.Tensor) -> bool:
-    return t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:-1])
+def _aligned(t: torch.Tensor, elems: int = 8) -> bool:
+    return t.data_ptr() % 16 == 0 and all(s % elems == 0 for s in t.stride()[:-1])
+
+
+def _scale_layout(kv_scale, lead: int, rows: int, device):
+    """float32 scale tensor of an fp8 cache and its (page, row) element strides.
+
+    lead = pages (paged cache) or sequences (dense), rows = rows per page
+    (or capacity). Accepted: one scale (a float or a one-element tensor),
+    [lead] (per page / sequence) or [lead, rows] (per token).
+    """
+    if not torch.is_tensor(kv_scale):
+        kv_scale = torch.tensor([float(kv_scale)])
+    kv_scale = kv_scale.to(device=device, dtype=torch.float32)
+    if kv_scale.numel() == 1:
+        return kv_scale.reshape(1).contiguous(), 0, 0
+    if kv_scale.dim() == 1:
+        assert kv_scale.shape[0] == lead, f"kv_scale of shape [{lead}] (per page) expected"
+        return kv_scale, kv_scale.stride(0), 0
+    assert kv_scale.dim() == 2 and tuple(kv_scale.shape) == (lead, rows), \
+        f"kv_scale of shape [{lead}, {rows}] (per token) expected"
+    return kv_scale, kv_scale.stride(0), kv_scale.stride(1)
 
 
 class DecodeLaunch:
@@ -76,7 +100,7 @@ class DecodeLaunch:
     """
 
     def __init__(self, q, kv_cache, cache_seqlens, block_table=None, head_dim_v=512,
-                 softmax_scale=None, num_splits=None, num_workers=None):
+                 softmax_scale=None, num_splits=None, num_workers=None, kv_scale=None):
         # validation mirrors kernel.py:235-245
         if kv_cache.dim() == 4:
             assert kv_cache.shape[2] == 1, "MLA uses a single shared latent KV head"
@@ -101,7 +125,14 @@ class DecodeLaunch:
         assert q.stride(-1) == 1 and kv_cache.stride(-1) == 1
         assert _next_power_of_2(head_dim_v) == head_dim_v
         assert _next_power_of_2(d_rope) == d_rope
-        assert q.dtype == kv_cache.dtype
+        fp8 = kv_cache.dtype in _FP8_CACHE
+        if fp8:
+            if kv_scale is None:
+                raise ValueError("an fp8 kv_cache needs kv_scale (its dequantisation scales)")
+            kv_cache = kv_cache.view(torch.uint8)
+        else:
+            assert kv_scale is None, "kv_scale applies to an fp8 (float8_e4m3fn) kv_cache only"
+            assert q.dtype == kv_cache.dtype
 
         if q.device.type != "cuda" or kv_cache.device != q.device:
             raise RuntimeError("triton_mla.mla_decode runs on the GPU only: q and kv_cache must be "
@@ -141,16 +172,24 @@ class DecodeLaunch:
         self.lse = torch.empty(*shape, dtype=torch.float32, device=device)
         vheads = q_len * num_heads  # rows of q / out per sequence
         self.fused = False
+        self.fp8 = fp8
         if batch == 0:
             return
         if num_blocks == 0:
             raise ValueError("kv_cache holds no tokens")
+        if fp8 and block_table is not None and page_size % 16 != 0:
+            raise NotImplementedError("an fp8 kv_cache needs pages of a multiple of 16 tokens")
         if not _aligned(q):
             q = q.contiguous()
-        if not _aligned(kv_cache):
+        if not _aligned(kv_cache, 16 if fp8 else 8):
             kv_cache = kv_cache.contiguous()
+        scale_args = ()
+        if fp8:
+            lead = kv_cache.shape[0]
+            kv_scale, sc0, sc1 = _scale_layout(kv_scale, lead, kv_cache.shape[1], device)
+            scale_args = (kv_scale.data_ptr(), sc0, sc1)
         # keep every tensor whose address is handed to the kernels alive
-        self._keep = (q, kv_cache, cache_seqlens, block_table)
+        self._keep = (q, kv_cache, cache_seqlens, block_table, kv_scale)
         self.lib = _native.load()
         self.splits = num_splits if num_splits is not None else 0
         # balanced partition: one worker per compute unit unless asked otherwise
@@ -169,7 +208,7 @@ class DecodeLaunch:
         # when all of its workgroups fit on the device at once, one per CU: the
         # library's own decision for these arguments
         capacity = (block_table.shape[1] * page_size) if block_table is not None else num_blocks
-        self.fused = bool(self.lib.tmla_mla_decode_fused_is_single(
+        self.fused = not fp8 and bool(self.lib.tmla_mla_decode_fused_is_single(
             batch, vheads, head_dim_v, self.splits, self.workers, capacity,
             device.index if device.index is not None else torch.cuda.current_device()))
         out_sh = self.out.stride(-2)  # one output row per (query token, head)
@@ -183,6 +222,10 @@ class DecodeLaunch:
         if q_len > 1:  # the same arguments with q_len before num_heads
             a = self._partial_args
             self._causal_args = a[:13] + (q_len,) + a[13:]
+        if fp8:  # the scale pointer and strides after page_size (and q_len)
+            a = self._partial_args
+            self._fp8_partial_args = a[:8] + scale_args + a[8:]
+            self._fp8_args = a[:8] + scale_args + a[8:13] + (q_len,) + a[13:]
         self._combine_args = (
             cache_seqlens.data_ptr(), batch, num_heads, head_dim_v, _native.DTYPE_CODE[q.dtype],
             self.splits, self.workers, self.out.data_ptr(), self.out.stride(0), self.out.stride(1),
@@ -197,8 +240,12 @@ class DecodeLaunch:
             raise NotImplementedError("multi-token queries run both stages at once (run())")
         if self.batch:
             with torch.cuda.device(self.device):
-                _native.check(self.lib.tmla_mla_decode_partial(*self._partial_args, self._stream()),
-                              "tmla_mla_decode_partial")
+                if self.fp8:
+                    _native.check(self.lib.tmla_mla_decode_fp8_partial(*self._fp8_partial_args, self._stream()),
+                                  "tmla_mla_decode_fp8_partial")
+                else:
+                    _native.check(self.lib.tmla_mla_decode_partial(*self._partial_args, self._stream()),
+                                  "tmla_mla_decode_partial")
 
     def combine(self):
         """Stage 2 on the current stream (tmla_mla_decode_combine)."""
@@ -219,8 +266,12 @@ class DecodeLaunch:
         """Both stages (tmla_mla_decode), or the single-launch form
         (tmla_mla_decode_fused) when single_launch is set. spin_limit: polls
         a worker of the in-kernel merge waits for its siblings before it hands
-        its share over (< 0: the library's default)."""
-        if self.batch and self.q_len > 1:
+        its share over (< 0: the library's default). An fp8 cache always
+        runs the two kernels."""
+        if self.batch and self.fp8:
+            with torch.cuda.device(self.device):
+                _native.check(self.lib.tmla_mla_decode_fp8(*self._fp8_args, self._stream()), "tmla_mla_decode_fp8")
+        elif self.batch and self.q_len > 1:
             with torch.cuda.device(self.device):
                 if single_launch:
                     self._clear_counters()
@@ -248,6 +299,7 @@ def mla_decode(
     num_splits: int = None,
     return_lse: bool = False,
     single_launch: bool = None,
+    kv_scale=None,
 ):
     """Weight-absorbed MLA decode attention over a shared latent KV cache.
 
@@ -274,12 +326,20 @@ def mla_decode(
         single_launch: merge the split partials inside the partial kernel
             (one launch instead of two, same bits) when its workgroups fit on
             the device at once; None selects DEFAULT_SINGLE_LAUNCH.
+        kv_scale: an extension for an fp8 cache (kv_cache of dtype
+            torch.float8_e4m3fn, or uint8 holding E4M3 codes): the float32
+            dequantisation scales, row value = e4m3 * scale -- one per page
+            ([num_blocks]; dense caches: [batch]), one per token
+            ([num_blocks, page_size]; dense: [batch, capacity]) or one for the
+            whole cache (a float or one-element tensor). Paged fp8 caches need
+            a page size that is a multiple of 16; they always run two kernels.
 
     Returns:
         out [batch, num_heads, head_dim_v] in q.dtype (and lse [batch,
         num_heads] float32).
     """
-    call = DecodeLaunch(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits)
+    call = DecodeLaunch(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits,
+                        kv_scale=kv_scale)
     out, lse = call.run(DEFAULT_SINGLE_LAUNCH if single_launch is None else single_launch)
     if return_lse:
         return out, lse
