@@ -51,19 +51,31 @@ namespace tmla {
 namespace f8 {
 
 constexpr int kSlice = 16;               // tokens per wave per 64-token tile
-constexpr int kStages = 4;               // ring entries per wave (3 slices in flight)
 constexpr int kHeads = 16;               // heads per workgroup: N of the MFMAs
 constexpr int kRow = 576;                // bytes per cache row (512 latent + 64 rope dims)
-constexpr int kKv = kSlice * kRow;       // 9216 bytes of rows per entry
+constexpr int kKv = kSlice * kRow;       // 9216 bytes of rows per ring entry
 constexpr int kEntry = kKv + 256;        // + token scales (64 lanes x 4 bytes, first 16 used)
-constexpr int kRing = kStages * kEntry;  // per wave
 constexpr int kOPitch = 512 * 4 + 16;    // merge staging: one fp32 row of a head, padded
-constexpr int kStats = 4 * kRing;        // per-wave max and sum of every head
-constexpr int kSmem = kStats + 2 * 4 * kHeads * 4;
 constexpr int kLoads = kKv / 1024 + 1;   // LDS-DMA instructions per slice (rows, scales)
-static_assert(4 * kHeads * kOPitch <= kStats, "merge staging fits the rings");
-static_assert(kSmem <= 160 * 1024, "LDS");
-static_assert(3 * kLoads < 64, "vmcnt range");
+
+// Launch shape: NW waves (4: one per SIMD; 8: two per SIMD, so that one
+// wave's MFMAs run under the other's VALU work), each with a ring of
+// STAGES entries; K operand reads KA and V^T reads VA ahead of their use
+// (fewer with two waves per SIMD, where registers are halved).
+template <int NW>
+struct F8Shape {
+  static_assert(NW == 4 || NW == 8, "waves per workgroup");
+  static constexpr int kStages = NW == 4 ? 4 : 2;
+  static constexpr int kTileStride = NW / 4;  // tiles between a wave's slices
+  static constexpr int KA = NW == 4 ? 9 : 3;
+  static constexpr int VA = NW == 4 ? 16 : 6;
+  static constexpr int kRing = kStages * kEntry;
+  static constexpr int kStats = NW * kRing;  // per-wave max and sum of every head
+  static constexpr int kSmem = kStats + 2 * NW * kHeads * 4;
+  static_assert(4 * kHeads * kOPitch <= kStats, "merge staging fits the rings");
+  static_assert(kSmem <= 160 * 1024, "LDS");
+  static_assert((kStages - 1) * kLoads < 64, "vmcnt range");
+};
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -180,7 +192,7 @@ struct F8Elt<TMLA_BF16> {
   }
   // (asm: see the note on MFMA forms below)
   __device__ static __forceinline__ void mfma_qk_first(f32x4& d, const v8& k, const v8& q) {
-    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(k), "v"(q));
+    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(k), "v"(q));
   }
   __device__ static __forceinline__ void mfma_qk(f32x4& d, const v8& k, const v8& q) {
     asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(k), "v"(q));
@@ -199,7 +211,7 @@ struct F8Elt<TMLA_FP16> {
     return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, HI);
   }
   __device__ static __forceinline__ void mfma_qk_first(f32x4& d, const v8& k, const v8& q) {
-    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=v"(d) : "v"(k), "v"(q));
+    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(k), "v"(q));
   }
   __device__ static __forceinline__ void mfma_qk(f32x4& d, const v8& k, const v8& q) {
     asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(d) : "v"(k), "v"(q));
@@ -210,16 +222,13 @@ struct F8Elt<TMLA_FP16> {
   __device__ static __forceinline__ _Float16 round(float x) { return (_Float16)x; }
 };
 
-// 16 fp8 bytes -> the two 8-element K operands (bytes 0-7, 8-15)
+// 8 fp8 bytes (two dwords) -> one 8-element K operand
 template <int DT>
-__device__ __forceinline__ void widen16(const i32x4& x, typename F8Elt<DT>::v8& lo, typename F8Elt<DT>::v8& hi) {
+__device__ __forceinline__ typename F8Elt<DT>::v8 widen8(int x, int y) {
   using E = F8Elt<DT>;
-  const auto a0 = E::template widen<false>(x[0]), a1 = E::template widen<true>(x[0]);
-  const auto b0 = E::template widen<false>(x[1]), b1 = E::template widen<true>(x[1]);
-  const auto c0 = E::template widen<false>(x[2]), c1 = E::template widen<true>(x[2]);
-  const auto d0 = E::template widen<false>(x[3]), d1 = E::template widen<true>(x[3]);
-  lo = typename E::v8{a0[0], a0[1], a1[0], a1[1], b0[0], b0[1], b1[0], b1[1]};
-  hi = typename E::v8{c0[0], c0[1], c1[0], c1[1], d0[0], d0[1], d1[0], d1[1]};
+  const auto a0 = E::template widen<false>(x), a1 = E::template widen<true>(x);
+  const auto b0 = E::template widen<false>(y), b1 = E::template widen<true>(y);
+  return typename E::v8{a0[0], a0[1], a1[0], a1[1], b0[0], b0[1], b1[0], b1[1]};
 }
 // 4 fp8 bytes -> one 4-element operand
 template <int DT>
@@ -229,13 +238,14 @@ __device__ __forceinline__ typename F8Elt<DT>::v4 widen4(int x) {
   return typename E::v4{a[0], a[1], b[0], b[1]};
 }
 
+// vmcnt: the copies of up to `pending` younger slices may stay in flight
+template <int MAXP>
 __device__ __forceinline__ void wait_slices(int pending) {
-  // vmcnt: the copies of up to `pending` younger slices may stay in flight
-  if (pending >= 3)
+  if (MAXP >= 3 && pending >= 3)
     wait_vmcnt<3 * kLoads>();
-  else if (pending == 2)
+  else if (MAXP >= 2 && pending >= 2)
     wait_vmcnt<2 * kLoads>();
-  else if (pending == 1)
+  else if (pending >= 1)
     wait_vmcnt<kLoads>();
   else
     wait_vmcnt<0>();
@@ -244,22 +254,28 @@ __device__ __forceinline__ void wait_slices(int pending) {
 }  // namespace f8
 
 // PAGED: block table (pages of a multiple of 16 tokens); else a dense
-// [batch, capacity, 576] cache.
-template <int DT, bool PAGED>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+// [batch, capacity, 576] cache. NW: waves per workgroup (F8Shape).
+template <int DT, bool PAGED, int NW>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void mla_partial_fp8_kernel(PartialArgs a) {
   using namespace f8;
   using E = F8Elt<DT>;
-  __shared__ __attribute__((aligned(1024))) char smem[kSmem];
+  using SH = F8Shape<NW>;
+  constexpr int kStages = SH::kStages;
+  constexpr int LEAD = kStages - 1;  // slices in flight ahead of the one computed
+  constexpr int KA = SH::KA, VA = SH::VA;
+  __shared__ __attribute__((aligned(1024))) char smem[SH::kSmem];
   char LDS_AS* const lds = (char LDS_AS*)(void LDS_AS*)smem;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sw = wave & 3;                   // slice of the tile: tokens 16 sw .. 16 sw + 15
+  const int par = wave >> 2;                 // first tile of the wave (NW = 8: tile parity)
   const int worker = worker_index(a);
   WorkRange wr;
   if (!work_range(a, worker, wr) || wr.tile_lo >= wr.tile_hi) return;
   const int head0 = blockIdx.y * kHeads;
   const int nh = min(kHeads, a.num_heads - head0);
-  char LDS_AS* const ring = lds + wave * kRing;
+  char LDS_AS* const ring = lds + wave * SH::kRing;
 
   int b = wr.b_first;
   int t_start = wr.tile_lo;              // local tile index within b
@@ -295,10 +311,14 @@ void mla_partial_fp8_kernel(PartialArgs a) {
       }
     }
 
-    // this wave's slices: tiles t_start .. t_end - 1, the last one only when
-    // its slice holds a token
-    const int ns = (t_end - t_start) - (kTileTokens * (t_end - 1) + kSlice * wave >= n_b ? 1 : 0);
-    auto slice_tok = [&](int k) __attribute__((always_inline)) { return kTileTokens * (t_start + k) + kSlice * wave; };
+    // this wave's slices: tiles t_start + par, + NW / 4, ... below t_end, the
+    // last one only when its slice holds a token
+    constexpr int TS = SH::kTileStride;
+    const int tiles_w = t_end - t_start - par > 0 ? (t_end - t_start - par + TS - 1) / TS : 0;
+    const int ns = tiles_w - (tiles_w > 0 && kTileTokens * (t_start + par + TS * (tiles_w - 1)) + kSlice * sw >= n_b ? 1 : 0);
+    auto slice_tok = [&](int k) __attribute__((always_inline)) {
+      return kTileTokens * (t_start + par + TS * k) + kSlice * sw;
+    };
     const int32_t* bt_row = PAGED ? a.bt + (int64_t)b * a.bt_sb : a.bt;
     auto page_fetch = [&](int k) __attribute__((always_inline)) -> int {
       return PAGED ? s_load_i32(bt_row + page_slot_of(a, slice_tok(k))) : 0;
@@ -321,7 +341,7 @@ void mla_partial_fp8_kernel(PartialArgs a) {
         sidx = (int64_t)b * a.sc_s0 + (int64_t)t * a.sc_s1;
       }
       const char* src = a.kv + row + g * 16;
-      char LDS_AS* dst = ring + (k & (kStages - 1)) * kEntry;
+      char LDS_AS* dst = ring + (k % kStages) * kEntry;
       static_for<kKv / 1024>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         lds_copy16<64 * j>(src, dst + 1024 * j);
@@ -344,71 +364,80 @@ void mla_partial_fp8_kernel(PartialArgs a) {
     // token 4g + j % 4 of chunk column 2u + j / 4
     const int tr_off = (((r >> 1) >> 2) * 16 + 4 * g + ((r >> 1) & 3)) * 16 + 8 * (r & 1);
 
-    // prologue: slices 0..2 in flight, page ids of slices 3 and 4 requested.
-    // Page ids come from scalar loads without a wait; every wait for them is
-    // an lgkmcnt(0) that names all ids still in flight, so none is read or
-    // moved before it has arrived.
-    int pg3 = 0, pg4 = 0;
+    // Prologue: slices 0 .. LEAD - 1 in flight, page ids of slices LEAD and
+    // LEAD + 1 requested. Page ids come from scalar loads without a wait;
+    // every wait for them is an lgkmcnt(0) that names all ids still in
+    // flight, so none is read or moved before it has arrived.
+    int pg_a = 0, pg_b = 0;  // page ids of slices k + LEAD and k + LEAD + 1
     {
-      int p0 = ns > 0 ? page_fetch(0) : 0;
-      int p1 = ns > 1 ? page_fetch(1) : 0;
-      int p2 = ns > 2 ? page_fetch(2) : 0;
-      pg3 = ns > 3 ? page_fetch(3) : 0;
-      pg4 = ns > 4 ? page_fetch(4) : 0;
-      if (PAGED) asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(p0), "+s"(p1), "+s"(p2), "+s"(pg3), "+s"(pg4));
-      if (ns > 0) issue(0, clamp_page(p0));
-      if (ns > 1) issue(1, clamp_page(p1));
-      if (ns > 2) issue(2, clamp_page(p2));
+      int p[LEAD];
+#pragma unroll
+      for (int i = 0; i < LEAD; ++i) p[i] = ns > i ? page_fetch(i) : 0;
+      pg_a = ns > LEAD ? page_fetch(LEAD) : 0;
+      pg_b = ns > LEAD + 1 ? page_fetch(LEAD + 1) : 0;
+      if (PAGED) {
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(pg_a), "+s"(pg_b));
+#pragma unroll
+        for (int i = 0; i < LEAD; ++i) asm volatile("" : "+s"(p[i]));
+      }
+#pragma unroll
+      for (int i = 0; i < LEAD; ++i)
+        if (ns > i) issue(i, clamp_page(p[i]));
     }
     // Q^T has arrived once the copies of the first slices are the only loads
     // in flight; from here on the compiler sees it as plain registers (no
     // load wait of its own inside the loop)
-    wait_slices(min(3, ns));
+    wait_slices<LEAD>(min(LEAD, ns));
 #pragma unroll
     for (int j = 0; j < 18; ++j) pin_v(qop[j]);
 
     for (int k = 0; k < ns; ++k) {
-      // the copies of slice k + 3 go into the entry slice k - 1 has left
-      if (k + 3 < ns) {
-        if (PAGED) asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(pg3), "+s"(pg4));
-        const int p = clamp_page(pg3);
-        pg3 = pg4;
-        issue(k + 3, p);
+      // the copies of slice k + LEAD go into the entry slice k - 1 has left
+      if (k + LEAD < ns) {
+        if (PAGED) asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(pg_a), "+s"(pg_b));
+        const int pcur = clamp_page(pg_a);
+        pg_a = pg_b;
+        issue(k + LEAD, pcur);
       }
-      wait_slices(min(3, ns - 1 - k));
-      const char LDS_AS* ent = ring + (k & (kStages - 1)) * kEntry;
+      wait_slices<LEAD>(min(LEAD, ns - 1 - k));
+      const char LDS_AS* ent = ring + (k % kStages) * kEntry;
       const int t0 = slice_tok(k);
 
-      // ---- S^T = K . Q^T, with the V^T reads of this slice issued beside it ----
-      // LDS operations in program order: token scales, K operands 0..8, then
-      // V^T reads 2j, 2j + 1 after step j; the wait of step j counts the
-      // reads younger than K operand j.
+      // ---- S^T = K . Q^T ----------------------------------------------------
+      // LDS operations in program order: token scales, K operands 0 .. KA - 1,
+      // then K operand j + KA after step j; the wait of step j counts the K
+      // reads younger than operand j. Each operand is widened right after the
+      // MFMA before it has issued (the scheduling barriers keep this order).
       f32x4 tsc = __builtin_bit_cast(f32x4, ds_read_x4<kKv>(ent + 16 * g));
       const char LDS_AS* kp = ent + 16 * lane;
       const char LDS_AS* vp = ent + tr_off;
       i32x4 kr[9];
-      i32x2 vr[16];
-      static_for<9>([&](auto jc) {
+      static_for<KA>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         kr[j] = ds_read_x4<1024 * j>(kp);
       });
       f32x4 s;
       static_for<9>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        lgkm_tie<(8 + j < 15 ? 8 + j : 15)>(kr[j]);
+        constexpr int younger = (KA - 1 < 8 - j) ? KA - 1 : 8 - j;
+        lgkm_tie<younger>(kr[j]);
         if constexpr (j == 0) pin_v(tsc);  // older than K operand 0: complete
-        typename E::v8 k0, k1;
-        widen16<DT>(kr[j], k0, k1);
+        const typename E::v8 k0 = widen8<DT>(kr[j][0], kr[j][1]);
         if constexpr (j == 0)
           E::mfma_qk_first(s, k0, qop[0]);
         else
           E::mfma_qk(s, k0, qop[2 * j]);
-        E::mfma_qk(s, k1, qop[2 * j + 1]);
-        if constexpr (j < 8) {
-          vr[2 * j] = ds_read_tr8<1024 * j>(vp);
-          vr[2 * j + 1] = ds_read_tr8<1024 * j + 512>(vp);
-        }
         __builtin_amdgcn_sched_barrier(0);
+        const typename E::v8 k1 = widen8<DT>(kr[j][2], kr[j][3]);
+        E::mfma_qk(s, k1, qop[2 * j + 1]);
+        if constexpr (j + KA < 9) kr[j + KA] = ds_read_x4<1024 * (j + KA)>(kp);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      // V^T reads 0 .. VA - 1 now, the rest one per value step
+      i32x2 vr[16];
+      static_for<VA>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        vr[u] = ds_read_tr8<512 * u>(vp);
       });
 
       // ---- online softmax (base 2) ---------------------------------------
@@ -434,16 +463,21 @@ void mla_partial_fp8_kernel(PartialArgs a) {
       l_run += (p[0] + p[1]) + (p[2] + p[3]);
       const typename E::v4 pb{E::round(p[0] * tsc[0]), E::round(p[1] * tsc[1]), E::round(p[2] * tsc[2]),
                               E::round(p[3] * tsc[3])};
-      // the page id of slice k + 5 is requested here, long before the wait
-      // for it (top of iteration k + 2 or later)
-      if (k + 5 < ns) pg4 = page_fetch(k + 5);
+      // the page id of slice k + LEAD + 2 is requested here, long before the
+      // wait for it (top of iteration k + 2)
+      if (k + LEAD + 2 < ns) pg_b = page_fetch(k + LEAD + 2);
       __builtin_amdgcn_sched_barrier(0);
 
       // ---- O^T += V^T . P^T ------------------------------------------------
+      // V^T read u + VA is issued once read u has been awaited: the wait of
+      // step u counts the VA - 1 reads after it (fewer at the end)
       static_for<16>([&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        lgkm_tie<15 - u>(vr[u]);
+        constexpr int younger = (VA - 1 < 15 - u) ? VA - 1 : 15 - u;
+        lgkm_tie<younger>(vr[u]);
+        if constexpr (u + VA < 16) vr[u + VA] = ds_read_tr8<512 * (u + VA)>(vp);
         E::mfma_pv(o[2 * u], widen4<DT>(vr[u][0]), pb);
+        __builtin_amdgcn_sched_barrier(0);
         E::mfma_pv(o[2 * u + 1], widen4<DT>(vr[u][1]), pb);
         __builtin_amdgcn_sched_barrier(0);
       });
@@ -451,37 +485,53 @@ void mla_partial_fp8_kernel(PartialArgs a) {
       for (int j = 0; j < 18; ++j) pin_v(qop[j]);
     }
 
-    // ---- merge the four waves and store --------------------------------------
+    // ---- merge the waves and store -------------------------------------------
     mfma_fence_a(o[31]);  // the last value products have landed
     {
       const float l_tot = rows_sum(l_run);
-      float LDS_AS* stats = reinterpret_cast<float LDS_AS*>(lds + kStats);  // [2][wave][head]
+      float LDS_AS* stats = reinterpret_cast<float LDS_AS*>(lds + SH::kStats);  // [2][wave][head]
       if (g == 0) {
         stats[wave * kHeads + r] = m_ref;
-        stats[4 * kHeads + wave * kHeads + r] = l_tot;
+        stats[NW * kHeads + wave * kHeads + r] = l_tot;
       }
       __syncthreads();  // every wave is past its loop: the rings are free
-      float mw[4], lw[4];
+      float M = kNoMax;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        mw[w] = stats[w * kHeads + r];
-        lw[w] = stats[4 * kHeads + w * kHeads + r];
-      }
-      const float M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, stats[w * kHeads + r]);
       float L = 0.0f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) L += fast_exp2(mw[w] - M) * lw[w];
+      for (int w = 0; w < NW; ++w) L += fast_exp2(stats[w * kHeads + r] - M) * stats[NW * kHeads + w * kHeads + r];
       const bool has = L > 0.0f;
       const float f = has ? fast_exp2(m_ref - M) / L : 0.0f;
-      // this wave's share of O^T, normalised: row = head, column = dim
-      char LDS_AS* stage = lds + wave * kHeads * kOPitch + r * kOPitch + 16 * g;
+      // staging region q of 4 holds one normalised O^T share: row = head,
+      // column = dim; with eight waves, wave q + 4 first hands its share to
+      // wave q through region q
+      char LDS_AS* stage = lds + (wave & 3) * kHeads * kOPitch + r * kOPitch + 16 * g;
+      if constexpr (NW == 8) {
+        if (wave >= 4) {
 #pragma unroll
-      for (int d = 0; d < 32; ++d) *reinterpret_cast<f32x4 LDS_AS*>(stage + 64 * d) = o[d] * f;
+          for (int d = 0; d < 32; ++d) *reinterpret_cast<f32x4 LDS_AS*>(stage + 64 * d) = o[d] * f;
+        }
+        __syncthreads();
+        if (wave < 4) {
+#pragma unroll
+          for (int d = 0; d < 32; ++d) o[d] = o[d] * f + *reinterpret_cast<const f32x4 LDS_AS*>(stage + 64 * d);
+        }
+        __syncthreads();
+        if (wave < 4) {
+#pragma unroll
+          for (int d = 0; d < 32; ++d) *reinterpret_cast<f32x4 LDS_AS*>(stage + 64 * d) = o[d];
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < 32; ++d) *reinterpret_cast<f32x4 LDS_AS*>(stage + 64 * d) = o[d] * f;
+      }
       __syncthreads();
-      // wave w writes heads 4w .. 4w + 3: lane l dims 8l .. 8l + 7
+      // wave w writes heads w * 16 / NW ..: lane l dims 8l .. 8l + 7
+      constexpr int HPW = kHeads / NW;
 #pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        const int hr = 4 * wave + hh;
+      for (int hh = 0; hh < HPW; ++hh) {
+        const int hr = HPW * wave + hh;
         f32x4 v0 = {0.0f, 0.0f, 0.0f, 0.0f}, v1 = v0;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -518,9 +568,18 @@ void mla_partial_fp8_kernel(PartialArgs a) {
   }
 }
 
+// Waves per workgroup (build-time knob, F8Shape): 4 by default. The
+// two-waves-per-SIMD form hides one wave's MFMAs under the other's VALU
+// work, but its two-entry rings leave one slice in flight per wave, and on
+// the 16-head ragged workload it measured 130.5 us against 114.4 us.
+#ifndef TMLA_FP8_WAVES
+#define TMLA_FP8_WAVES 4
+#endif
+
 template <int DT, bool PAGED>
 hipError_t launch_fp8_t(const PartialArgs& a, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((mla_partial_fp8_kernel<DT, PAGED>), grid, dim3(256), 0, stream, a);
+  constexpr int NW = TMLA_FP8_WAVES;
+  hipLaunchKernelGGL((mla_partial_fp8_kernel<DT, PAGED, NW>), grid, dim3(64 * NW), 0, stream, a);
   return hipGetLastError();
 }
 
