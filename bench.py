@@ -21,6 +21,12 @@ beside it with min / median / p90. After the timed region, the public
 host-side argument checks included) is timed the way the reference's bench
 times it.
 
+Then the fp8-cache leg (``fp8_cache`` in the JSON line; ``--no-fp8`` skips
+it): the 16-head ragged workload (B=64, 1K..32K tokens, page 64) with its
+cache quantised to E4M3 with one float32 scale per page, timed interleaved
+with the bf16 decode of the unquantised cache (two-kernel steps and partial
+kernels alone), with the fp8 partial kernel's roofline over the fp8 bytes.
+
 ``--copy-mib N`` adds, after the timed steps, three device-to-device copies
 of N MiB: kernels of known traffic against which the HBM counters of a
 profiler run (FETCH_SIZE, WRITE_SIZE) are scaled.
@@ -59,6 +65,7 @@ def parse():
                    help="'balanced' (device-side tile balancing) or an integer split count")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on each CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-fp8", action="store_true", help="skip the fp8-cache leg (16-head ragged workload)")
     p.add_argument("--no-flush", action="store_true", help="do not evict caches between steps")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="after timing, run 3 copies of this many MiB (counter calibration)")
@@ -102,6 +109,68 @@ def cpu_baseline(inp, target_s):
     t_torch = timed(mla_decode_torch, n_torch)
     return {"cores": cores, "n_ref": n_ref, "t_ref": t_ref, "n_torch": n_torch, "t_torch": t_torch,
             "out_ref": out_ref}
+
+
+def fp8_leg(args, dev, flush, stream):
+    """The fp8 (E4M3, one scale per page) cache on the 16-head ragged
+    workload (B=64, 1K..32K tokens, page 64): the two-kernel step and the
+    partial kernel alone, interleaved with the bf16 decode of the same
+    cache before quantisation."""
+    import torch
+
+    from triton_mla import quantize_kv_fp8, workloads
+    from triton_mla.kernel import DecodeLaunch
+
+    host = workloads.ragged_b64_h16()
+    g = host.to(dev)
+    codes, scale = quantize_kv_fp8(g.kv_cache, "page")
+    c8 = DecodeLaunch(g.q, codes, g.seqlens, g.block_table, 512, host.softmax_scale, None, kv_scale=scale)
+    c16 = DecodeLaunch(g.q, g.kv_cache, g.seqlens, g.block_table, 512, host.softmax_scale, None)
+    forms = {"fp8_step": c8.run, "fp8_partial": c8.partial, "bf16_step": c16.run, "bf16_partial": c16.partial}
+    for _ in range(max(args.warmup // 2, 2)):
+        for fn in forms.values():
+            if flush:
+                flush()
+            fn()
+    steps = max(args.steps // 2, 10)
+    ev = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+          for k in forms}
+    torch.cuda.synchronize(dev)
+    for i in range(steps):
+        for k, fn in forms.items():
+            if flush:
+                flush()
+            ev[k][i][0].record(stream)
+            fn()
+            ev[k][i][1].record(stream)
+    torch.cuda.synchronize(dev)
+    us = {k: [a.elapsed_time(b) * 1e3 for a, b in v] for k, v in ev.items()}
+    c8.run()
+    torch.cuda.synchronize(dev)
+    tokens = int(host.seqlens.sum())
+    q_out = host.q.numel() * 2 + host.batch * host.heads * 512 * 2
+    bytes8 = tokens * 576 + scale.numel() * 4 + q_out
+    bytes16 = host.algorithmic_bytes()
+    med = {k: statistics.median(v) for k, v in us.items()}
+    p8 = statistics.fmean(us["fp8_partial"])
+    summary = {
+        "workload": host.name, "batch": host.batch, "heads": host.heads, "tokens": tokens, "page_size": 64,
+        "format": "e4m3 codes + float32 scale per page", "algorithmic_bytes": bytes8,
+        "step_us": {k: spread(v) for k, v in us.items()},
+        "roofline": {"bound": "hbm", "kernel": "mla_partial_fp8_kernel", "partial_us_mean": round(p8, 2),
+                     "achieved": round(bytes8 / (p8 * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(bytes8 / (p8 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "step_frac": round(bytes8 / (med["fp8_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+        "bf16_same_workload": {"algorithmic_bytes": bytes16,
+                               "step_frac": round(bytes16 / (med["bf16_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+        "speedup_vs_bf16_step": round(med["bf16_step"] / med["fp8_step"], 3),
+    }
+    gate = {"q": host.q, "codes": codes.view(torch.uint8).cpu().numpy(), "scale": scale.cpu().numpy(),
+            "seqlens": host.seqlens.numpy(), "bt": host.block_table.numpy(), "softmax_scale": host.softmax_scale,
+            "out": c8.out.cpu()}
+    del c8, c16, g, codes, scale
+    torch.cuda.empty_cache()
+    return {"summary": summary, "gate": gate}
 
 
 def main():
@@ -209,6 +278,8 @@ def main():
     except RuntimeError as exc:  # capture unsupported in this environment
         print(f"graph capture failed: {exc}", file=sys.stderr)
 
+    fp8 = None if args.no_fp8 else fp8_leg(args, dev, flush, stream)
+
     if args.copy_mib > 0:
         src = torch.ones(args.copy_mib << 18, dtype=torch.int32, device=dev)
         dst = torch.empty_like(src)
@@ -262,6 +333,8 @@ def main():
         "timed_launches": {k: args.steps for k in us},
         "graph_replay_matches_eager": graph_ok,
     }
+    if fp8 is not None:
+        result["fp8_cache"] = fp8["summary"]
 
     if not args.no_cpu_baseline:
         import numpy as np
@@ -298,6 +371,16 @@ def main():
         if cb["out_ref"] is not None:
             result["cpu_baseline"]["gpu_vs_cpu_ref_max_abs_err"] = \
                 (eager_out.float().cpu() - cb["out_ref"].float()).abs().max().item()
+        if fp8 is not None:
+            # the fp8 leg's gate: the float64 fp8 oracle on its first two sequences
+            f = fp8["gate"]
+            ref8, _ = oracle.mla_decode_fp8_ref(u16(f["q"][:n]), f["codes"], f["scale"], f["seqlens"][:n],
+                                                f["bt"][:n], 512, f["softmax_scale"])
+            err8 = (f["out"][:n].float() - torch.from_numpy(ref8)).abs().max().item()
+            if not err8 <= 1e-2:
+                print(f"fp8 correctness gate failed: max |gpu - oracle| = {err8}", file=sys.stderr)
+                sys.exit(1)
+            result["fp8_cache"]["gpu_vs_oracle_max_abs_err"] = err8
     print(json.dumps(result), flush=True)
 
 

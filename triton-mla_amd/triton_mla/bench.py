@@ -10,7 +10,7 @@ column keeps its name for drop-in CSV consumers and holds the HIP kernels'
 time; ``config`` names the launch shape that ran. Additions: --workload runs
 the named seeded workloads of triton_mla.workloads (uniform and ragged
 lengths), --splits picks the split scheme, --no-compile skips torch.compile,
---layer times one decode step of the whole MLA layer at DeepSeek-V3 dims
+--kv-fp8 decodes an E4M3 copy of the cache, --layer times one decode step of the whole MLA layer at DeepSeek-V3 dims
 (random N(0, 0.02) bf16 weights, --batch sequences of --seqlen cached tokens)
 with the HIP glue (MLA.forward) and with the reference's torch glue
 (MLA.forward_torch_glue) around the same mla_decode.
@@ -31,6 +31,7 @@ import os
 import torch
 
 from . import workloads
+from .fp8 import dequantize_kv_fp8, quantize_kv_fp8
 from .kernel import DecodeLaunch, _num_sms
 from .reference import mla_decode_torch
 from .timing import Flusher, time_us
@@ -58,13 +59,22 @@ def _splits_arg(text):
 
 def bench_one(inp, args, device, flush, compiled, writer, gpu):
     splits = _splits_arg(args.splits)
-    call = DecodeLaunch(inp.q, inp.kv_cache, inp.seqlens, inp.block_table, 512, inp.softmax_scale, splits)
+    torch_cache = inp.kv_cache
+    if args.kv_fp8 != "none":
+        # the HIP decode reads the E4M3 cache; the PyTorch baselines decode the
+        # same values dequantised to the input dtype
+        codes, scale = quantize_kv_fp8(inp.kv_cache, args.kv_fp8)
+        torch_cache = dequantize_kv_fp8(codes, scale).to(inp.q.dtype)
+        call = DecodeLaunch(inp.q, codes, inp.seqlens, inp.block_table, 512, inp.softmax_scale, splits,
+                            kv_scale=scale)
+    else:
+        call = DecodeLaunch(inp.q, inp.kv_cache, inp.seqlens, inp.block_table, 512, inp.softmax_scale, splits)
     call.run()
     torch.cuda.synchronize(device)
     out = call.out
 
     def run_torch(fn):
-        return fn(inp.q, inp.kv_cache, inp.seqlens, inp.block_table, softmax_scale=inp.softmax_scale)
+        return fn(inp.q, torch_cache, inp.seqlens, inp.block_table, softmax_scale=inp.softmax_scale)
 
     t_compile = None
     if compiled is not None:
@@ -84,11 +94,17 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
                           device=device)["median"]
 
     nbytes = inp.algorithmic_bytes()
+    if args.kv_fp8 != "none":  # one byte per cache element (+ the scales)
+        tokens = int(inp.seqlens.sum())
+        nbytes -= tokens * 576
+        nbytes += (scale.numel() * 4)
     flops = inp.flops()
     workers = call.workers or call.splits * inp.batch
     # (the heads per workgroup are chosen inside the library from the call's
     # shape, so the label names the partition only)
     config = "hip/" + (f"balanced{workers}" if splits is None else f"splits{splits}")
+    if args.kv_fp8 != "none":
+        config += f"/fp8-{args.kv_fp8}"
     seqlen = int(inp.seqlens.max())
     row = [inp.batch, seqlen, args.splits, config, f"{t_hip:.1f}", f"{nbytes / t_hip / 1e6:.2f}",
            f"{flops / t_hip / 1e6:.0f}"]
@@ -160,6 +176,9 @@ def main(argv=None):
                         help="run these named workloads instead of the --batch x --seqlen grid")
     parser.add_argument("--splits", default="balanced", help="'balanced' or a per-sequence split count")
     parser.add_argument("--reps", type=int, default=100)
+    parser.add_argument("--kv-fp8", choices=["none", "page", "token", "tensor"], default="none",
+                        help="decode an E4M3 copy of the cache (scales per page, token or tensor); the "
+                             "PyTorch baselines decode the dequantised values")
     parser.add_argument("--layer", action="store_true",
                         help="time the MLA layer step at DeepSeek-V3 dims (HIP glue vs torch glue)")
     args = parser.parse_args(argv)
