@@ -113,6 +113,15 @@ CASES = {
     "h20_two_head_groups": (2, 20, [129, 3000], 64, "token", False, torch.bfloat16, 2),
     "h16_fp16_q": (2, 16, [513, 90], 64, "page", False, torch.float16, None),
     "empty_and_short": (3, 16, [0, 50, 0], 64, "page", False, torch.bfloat16, None),
+    # more than 16 heads, one scale per page or per tensor, pages of whole
+    # 32-token sub-tiles: the cache widened once per workgroup into the
+    # 16-bit kernel's ring (1, 2 and 4 head blocks per workgroup)
+    "ring_h128_ragged_page64": (6, 128, [1, 15, 16, 17, 1000, 4103], 64, "page", False, torch.bfloat16, None),
+    "ring_h64_page32_tensor_scale": (3, 64, [31, 32, 2500], 32, "tensor", False, torch.bfloat16, None),
+    "ring_h32_page128_splits3": (4, 32, [128, 129, 700, 3000], 128, "page", False, torch.bfloat16, 3),
+    "ring_h128_fp16_q_unsplit": (2, 128, [300, 64], 64, "page", False, torch.float16, 1),
+    "ring_h48_partial_head_block": (2, 48, [900, 33], 64, "page", False, torch.bfloat16, None),
+    "ring_h128_many_workers": (16, 128, [4096] * 16, 64, "page", False, torch.bfloat16, None),
 }
 
 
@@ -199,6 +208,44 @@ def test_fp8_full_size_h16_ragged(gpu):
     torch.cuda.synchronize()
     np.testing.assert_allclose(out.float().cpu().numpy(), ref[0], atol=1e-2, rtol=1e-2)
     np.testing.assert_allclose(lse.cpu().numpy(), ref[1], atol=1e-5, rtol=1e-5)
+
+
+def test_fp8_ring_matches_bf16_kernel_on_exact_cache(gpu):
+    """128 heads (the widened ring): with power-of-two page scales the fp8
+    and bf16 decodes see the same cache values; both meet the budget around
+    the same oracle result."""
+    from triton_mla import dequantize_kv_fp8, mla_decode
+
+    q, codes, amax_scale, lens, bt = _make(3, 128, [64, 1000, 2049], 64, "page", seed=21)
+    scale = 2.0 ** torch.floor(torch.log2(amax_scale))
+    kv16 = dequantize_kv_fp8(codes, scale).to(torch.bfloat16)
+    sm = 576 ** -0.5
+    ref = _oracle(q, codes, scale, lens, bt, sm)
+    o8, l8 = mla_decode(q.to(gpu), codes.to(gpu), lens.to(gpu), bt.to(gpu), softmax_scale=sm, return_lse=True,
+                        kv_scale=scale.to(gpu))
+    o16, l16 = mla_decode(q.to(gpu), kv16.to(gpu), lens.to(gpu), bt.to(gpu), softmax_scale=sm, return_lse=True)
+    torch.cuda.synchronize()
+    _check(o8, l8, ref, q, codes, scale, lens, bt, sm, split=True)
+    _check(o16, l16, ref, q, codes, scale, lens, bt, sm, split=True)
+
+
+def test_fp8_ring_full_size_h128(gpu):
+    """The 32-sequence, 8K-token, 128-head workload with a per-page-scaled fp8
+    cache (the widened ring); the first four sequences against the oracle
+    (every output is checked for finiteness)."""
+    from triton_mla import mla_decode, quantize_kv_fp8, workloads
+
+    inp = workloads.b32_h128_8k()
+    codes, scale = quantize_kv_fp8(inp.kv_cache, "page")
+    print(f"B={inp.batch} H={inp.heads} tokens={int(inp.seqlens.sum())}", flush=True)
+    out, lse = mla_decode(inp.q.to(gpu), codes.to(gpu), inp.seqlens.to(gpu), inp.block_table.to(gpu),
+                          softmax_scale=inp.softmax_scale, return_lse=True, kv_scale=scale.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    n = 4
+    ref = _oracle(inp.q[:n], codes, scale, inp.seqlens[:n], inp.block_table[:n], inp.softmax_scale)
+    _check(out[:n], lse[:n], ref, inp.q[:n], codes, scale, inp.seqlens[:n], inp.block_table[:n], inp.softmax_scale,
+           split=True)
 
 
 def test_fp8_argument_errors(gpu):

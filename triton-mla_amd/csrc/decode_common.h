@@ -104,6 +104,9 @@ __device__ __forceinline__ int s_load_i32(const int32_t* p) {
   asm volatile("s_load_dword %0, %1, 0x0" : "=s"(r) : "s"(p));
   return r;
 }
+__device__ __forceinline__ float s_load_f32(const float* p) {
+  return __builtin_bit_cast(float, s_load_i32(reinterpret_cast<const int32_t*>(p)));
+}
 __device__ __forceinline__ int s_wait_i32(int v) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v));
   return v;

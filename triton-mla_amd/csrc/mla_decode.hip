@@ -77,12 +77,33 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 #ifndef TMLA_WAIT_PAIR
 #define TMLA_WAIT_PAIR 1
 #endif
+// step order inside a pass: 0 = reads, wait, S MFMA, PV MFMA, hook;
+// 1 = wait, S MFMA, reads, hook, PV MFMA (the two MFMAs of a step apart)
+#ifndef TMLA_STEP_ORDER
+#define TMLA_STEP_ORDER 0
+#endif
+// 1: the S and PV MFMAs are volatile asm, so they keep their places among
+// the LDS reads and waits instead of being grouped by the scheduler
+#ifndef TMLA_MFMA_VOLATILE
+#define TMLA_MFMA_VOLATILE 0
+#endif
+// 1: probabilities rounded two at a time (v_cvt_pk_*_f32, same rounding)
+#ifndef TMLA_PACK_PK
+#define TMLA_PACK_PK 1
+#endif
 // 1: phase stamps (profiling builds only; see tmla_debug_stamps)
 #ifndef TMLA_STAMPS
 #define TMLA_STAMPS 0
 #endif
 constexpr int kStages = 4;          // LDS ring depth (3 sub-tiles in flight)
 constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
+// fp8 cache: up to this many heads the 16-head-group kernel runs (its
+// workgroups stream the cache on their own); above, the 16-bit kernel with the
+// cache widened once per workgroup into its ring
+#ifndef TMLA_FP8_GROUP_HEADS
+#define TMLA_FP8_GROUP_HEADS 16
+#endif
+constexpr int kFp8GroupHeads = TMLA_FP8_GROUP_HEADS;
 
 struct CombineArgs {
   const int32_t* seqlens;
@@ -237,21 +258,80 @@ constexpr int pass_reads(int t) {
 template <int DT>
 __device__ __forceinline__ f32x16 mfma_vgpr_first(const i16x8& a, const i16x8& b) {
   f32x16 d;
-  if constexpr (DT == TMLA_BF16)
-    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
-  else
-    asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+  if constexpr (TMLA_MFMA_VOLATILE) {
+    if constexpr (DT == TMLA_BF16)
+      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+    else
+      asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  } else {
+    if constexpr (DT == TMLA_BF16)
+      asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+    else
+      asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+  }
   return d;
 }
 template <int DT>
 __device__ __forceinline__ void mfma_vgpr_acc(f32x16& d, const i16x8& a, const i16x8& b) {
-  if constexpr (DT == TMLA_BF16)
-    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
-  else
-    asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  if constexpr (TMLA_MFMA_VOLATILE) {
+    if constexpr (DT == TMLA_BF16)
+      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+    else
+      asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  } else {
+    if constexpr (DT == TMLA_BF16)
+      asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+    else
+      asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  }
+}
+// O^T += V^T . P^T with the accumulator in AGPRs. The volatile asm form
+// keeps its place among the reads and waits; its operands come straight
+// from LDS reads (no VALU writes them just before), and the accumulators are
+// read by VALU code only after mfma_agpr_fence or long after their last MFMA
+// (the lazy rescale, one softmax and one barrier later).
+template <int DT>
+__device__ __forceinline__ void mfma_agpr_acc(f32x16& acc, const i16x8& v, const i16x8& p) {
+  if constexpr (TMLA_MFMA_VOLATILE) {
+    if constexpr (DT == TMLA_BF16)
+      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(v), "v"(p));
+    else
+      asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(v), "v"(p));
+  } else {
+    acc = Elt<DT>::mfma(v, p, acc);
+    asm volatile("" : "+a"(acc));
+  }
+}
+__device__ __forceinline__ void mfma_agpr_fence(f32x16& acc) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(acc));
 }
 __device__ __forceinline__ void mfma_vgpr_fence(f32x16& d) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(d));
+}
+
+// Exact widening of 8 fp8 (e4m3) bytes, half H of a 16-byte chunk, to 8
+// elements of the 16-bit type (every e4m3 value is a bf16 and an fp16 value;
+// the conversion's scale is 1).
+template <int DT, int H>
+__device__ __forceinline__ i16x8 widen_half(const i16x8& raw) {
+  typedef int i32x4v __attribute__((ext_vector_type(4)));
+  const i32x4v x = __builtin_bit_cast(i32x4v, raw);
+  const int lo = x[2 * H], hi = x[2 * H + 1];
+  if constexpr (DT == TMLA_BF16) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 a0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+    const b2 a1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+    const b2 b0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+    const b2 b1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+    return __builtin_bit_cast(i16x8, bf16x8{a0[0], a0[1], a1[0], a1[1], b0[0], b0[1], b1[0], b1[1]});
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 a0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false);
+    const h2 a1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true);
+    const h2 b0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false);
+    const h2 b1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true);
+    return __builtin_bit_cast(i16x8, f16x8{a0[0], a0[1], a1[0], a1[1], b0[0], b0[1], b1[0], b1[1]});
+  }
 }
 
 // Two probabilities rounded to the 16-bit type, packed into one dword (a in
@@ -261,8 +341,18 @@ __device__ __forceinline__ void mfma_vgpr_fence(f32x16& d) {
 // own: registers 0-3 hold the first token half, 4-7 the second.
 template <int DT>
 __device__ __forceinline__ float pack_pair(float a, float b) {
-  const unsigned lo = (unsigned short)Elt<DT>::from_float(a), hi = (unsigned short)Elt<DT>::from_float(b);
-  return __builtin_bit_cast(float, lo | (hi << 16));
+  if constexpr (TMLA_PACK_PK) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    if constexpr (DT == TMLA_BF16)
+      return __builtin_bit_cast(float, __builtin_convertvector((f32x2){a, b}, bf16x2));
+    else
+      return __builtin_bit_cast(float, __builtin_convertvector((f32x2){a, b}, f16x2));
+  } else {
+    const unsigned lo = (unsigned short)Elt<DT>::from_float(a), hi = (unsigned short)Elt<DT>::from_float(b);
+    return __builtin_bit_cast(float, lo | (hi << 16));
+  }
 }
 template <int DT>
 __device__ __forceinline__ void pack_probs_in_place(f32x16& p) {
@@ -613,7 +703,15 @@ struct Segment {
 // With fewer than 4 head blocks the waves past NHB only copy and run PV, so
 // small head counts still use every SIMD of the CU.
 // PAGE_UNIFORM: paged, page size a power of two and a multiple of 32
-template <int DT, int DV, int DR, int NHB, bool PAGED, bool PAGE_UNIFORM>
+// F8: the cache holds fp8 (e4m3) codes with one float32 scale per page (or
+// per tensor), pages of a multiple of 32 tokens. Each wave copies the fp8
+// bytes of its 8 rows of a sub-tile into its own staging slot (LDS-DMA, half
+// the bytes of a 16-bit row) and widens them, exactly, into the same 16-bit
+// ring layout the 16-bit cache is copied into, once for all heads of the
+// workgroup; the page's scale multiplies the scores (folded into the softmax
+// scale) and the probabilities before their rounding. The V ring has three
+// entries and the rope ring two, which makes room for two staging entries.
+template <int DT, int DV, int DR, int NHB, bool PAGED, bool PAGE_UNIFORM, bool F8 = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void mla_partial_kernel(PartialArgs a) {
   constexpr int DQK = DV + DR;
@@ -628,11 +726,16 @@ void mla_partial_kernel(PartialArgs a) {
   constexpr int NACC = NDBW * NHB;        // 32x32 accumulator blocks per wave
   constexpr int VSLOT = 4 * NVB * 1024;   // V ring entry
   constexpr int RSLOT = 4 * NRB * 1024;   // rope ring entry
-  constexpr int kRopeStages = kStages - 1;
+  constexpr int VST = F8 ? 3 : kStages;   // V ring entries
+  constexpr int kRopeStages = VST - 1;    // rope ring entries
   constexpr int PSLOT = NHB * 2 * 1024;   // P^T of one sub-tile: [hb][c][lane] x 16 bytes
   constexpr int ASLOT = 32 * 4 * 4;       // per-head factors: [head % 32][hb] floats
-  constexpr int OFF_R = kStages * VSLOT;
-  constexpr int OFF_P = OFF_R + kRopeStages * RSLOT;
+  constexpr int STG_W = 8 * DQK;          // fp8 staging: one wave's 8 rows of a sub-tile
+  constexpr int STG = 4 * STG_W;          // ... one sub-tile
+  constexpr int LOADS8 = (STG_W + 1023) / 1024;  // fp8 DMA instructions per wave per sub-tile
+  constexpr int OFF_R = VST * VSLOT;
+  constexpr int OFF_S = OFF_R + kRopeStages * RSLOT;
+  constexpr int OFF_P = OFF_S + (F8 ? 2 * STG : 0);
   constexpr int OFF_A = OFF_P + 2 * PSLOT;
   constexpr int SMEM = OFF_A + 2 * ASLOT;
   constexpr int RG_PER_WAVE = 4 / NW;
@@ -643,6 +746,9 @@ void mla_partial_kernel(PartialArgs a) {
   static_assert(LOADS < 64, "vmcnt immediate range");
   static_assert(NHB * 32 * OPITCH <= OFF_P, "output staging fits the rings");
   static_assert(DV == 512, "one output row = 64 lanes x 8 elements");
+  static_assert(!F8 || (PAGED && PAGE_UNIFORM), "fp8 ring: pages of whole sub-tiles");
+  static_assert(!F8 || (DQK == 576 && LOADS8 == 5 && STG_W == 4608), "fp8 staging: 4 full copies + a half (rope)");
+  static_assert(SMEM <= 160 * 1024, "LDS");
 
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
   char LDS_AS* const lds = (char LDS_AS*)(void LDS_AS*)smem;
@@ -841,8 +947,67 @@ void mla_partial_kernel(PartialArgs a) {
 #pragma unroll
       for (int ri = 0; ri < RG_PER_WAVE; ++ri)
         static_for<NCB>([&](auto CB) __attribute__((always_inline)) {
-          copy_one(k % kStages * VSLOT, k % kRopeStages * RSLOT, ri, CB, src);
+          copy_one(k % VST * VSLOT, k % kRopeStages * RSLOT, ri, CB, src);
         });
+    };
+
+    // fp8 cache. Copy of one sub-tile: this wave's rows 8w .. 8w + 7 into its
+    // staging slot of entry (k & 1), where copy j (j < 4) moves the 16-byte
+    // chunks 8j + lane / 8 (dims 128j + 16 * (lane / 8) ..) of row lane % 8
+    // and copy 4 (lanes < 32) the rope chunks 32 + lane / 8. Lane l thus
+    // reads back exactly the chunks it copied, and their places in the ring
+    // differ from copy to copy by immediate offsets only.
+    // (lane-derived offsets are recomputed where used: kept across the loop
+    // they would not fit the register file beside Q^T and the operands)
+    auto issue8 = [&](int st, int page) __attribute__((always_inline)) {
+      const int k = st - st0;  // >= 0
+      const int ln = lane_id_fresh();
+      char LDS_AS* stg = lds + OFF_S + (k & 1) * STG + wave * STG_W;
+      const int tok_base = st * kSubTokens;
+      // a whole sub-tile of one page, or the sequence's last sub-tile, whose
+      // rows past its end read its last row
+      const int tok = min(tok_base + 8 * wave + (ln & 7), n_b - 1);
+      const char* src = a.kv + (int64_t)page * a.kv_s0 + (uint32_t)((tok & (a.page_size - 1)) * (uint32_t)a.kv_s1) +
+                        16 * (ln >> 3);
+      static_for<4>([&](auto J) __attribute__((always_inline)) {
+        constexpr int j = decltype(J)::value;
+        lds_copy16<128 * j>(src, stg + 1024 * j);
+      });
+      if (ln < 32) lds_copy16<512>(src, stg + 4096);
+    };
+    // Widening of the sub-tile copied into staging entry (k & 1) into V ring
+    // entry k % VST and rope ring entry k % (VST - 1): conv_read fetches this
+    // wave's chunks (its own copies: no barrier needed), conv_write writes
+    // them, exactly widened, in the 16-bit ring layout (after the barrier
+    // that frees the entries).
+    i16x8 raw8[5];
+    auto conv_read = [&](int k) __attribute__((always_inline)) {
+      const char LDS_AS* stg = lds + OFF_S + (k & 1) * STG + wave * STG_W + lane_id_fresh() * 16;
+      static_for<5>([&](auto J) __attribute__((always_inline)) {
+        constexpr int j = decltype(J)::value;
+        raw8[j] = ds_read_b128<1024 * j>(stg);
+      });
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(raw8[0]), "+v"(raw8[1]), "+v"(raw8[2]), "+v"(raw8[3]), "+v"(raw8[4]));
+    };
+    auto conv_write = [&](int k) __attribute__((always_inline)) {
+      const int ln = lane_id_fresh();
+      const int r8c = ln & 7;
+      const int swc = piece_swizzle(r8c, wave);
+      const int p0c = 2 * ((ln >> 3) & 3);
+      const int relA = (ln >> 5) * 1024 + (r8c * 8 + (p0c ^ swc)) * 16;
+      const int relB = (ln >> 5) * 1024 + (r8c * 8 + ((p0c + 1) ^ swc)) * 16;
+      char LDS_AS* vA = lds + (k % VST) * VSLOT + wave * NVB * 1024 + relA;
+      char LDS_AS* vB = lds + (k % VST) * VSLOT + wave * NVB * 1024 + relB;
+      static_for<4>([&](auto J) __attribute__((always_inline)) {
+        constexpr int j = decltype(J)::value;
+        ds_write_b128<2048 * j>(vA, widen_half<DT, 0>(raw8[j]));
+        ds_write_b128<2048 * j>(vB, widen_half<DT, 1>(raw8[j]));
+      });
+      if (ln < 32) {
+        char LDS_AS* r = lds + OFF_R + (k % kRopeStages) * RSLOT + wave * NRB * 1024;
+        ds_write_b128<0>(r + relA, widen_half<DT, 0>(raw8[4]));
+        ds_write_b128<0>(r + relB, widen_half<DT, 1>(raw8[4]));
+      }
     };
 
     // One pass over a sub-tile pair: S^T of the sub-tile in kst (DO_S) and
@@ -915,9 +1080,10 @@ void mla_partial_kernel(PartialArgs a) {
       static_for<PD>([&](auto T) __attribute__((always_inline)) { fetch(T); });
       static_for<NSTEPS>([&](auto J) __attribute__((always_inline)) {
         constexpr int j = decltype(J)::value;
-        if constexpr (j + PD < NSTEPS) fetch(std::integral_constant<int, j + PD>{});
-        // reads issued after those of step j
-        constexpr int last = (j + PD < NSTEPS - 1) ? j + PD : NSTEPS - 1;
+        if constexpr (!TMLA_STEP_ORDER && j + PD < NSTEPS) fetch(std::integral_constant<int, j + PD>{});
+        // reads issued after those of step j (before this step's wait)
+        constexpr int ahead = TMLA_STEP_ORDER ? PD - 1 : PD;
+        constexpr int last = (j + ahead < NSTEPS - 1) ? j + ahead : NSTEPS - 1;
         constexpr int after = [] {
           int n = 0;
           for (int t = j + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NHB, PVOFF, PVS>(t);
@@ -961,13 +1127,23 @@ void mla_partial_kernel(PartialArgs a) {
           else
             mfma_vgpr_acc<DT>(s, kb[r], qop[SLO + j]);
         }
-        if constexpr (pv) {
-          const i16x4 lo = vl[vi], hi4 = vh[vi];
-          const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-          acc[j4 * NHB + hb] = Elt<DT>::mfma(vop, pop[c][hb], acc[j4 * NHB + hb]);
-          pin_agpr(acc[j4 * NHB + hb]);
+        auto pv_mfma = [&]() __attribute__((always_inline)) {
+          if constexpr (pv) {
+            const i16x4 lo = vl[vi], hi4 = vh[vi];
+            const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+            mfma_agpr_acc<DT>(acc[j4 * NHB + hb], vop, pop[c][hb]);
+          }
+        };
+        if constexpr (TMLA_STEP_ORDER) {
+          // the reads of a later step and this step's hook run under the S
+          // MFMA, the PV MFMA follows them
+          if constexpr (j + PD < NSTEPS) fetch(std::integral_constant<int, j + PD>{});
+          hook(J);
+          pv_mfma();
+        } else {
+          pv_mfma();
+          hook(J);
         }
-        hook(J);
       });
       if constexpr (do_s && SHI == NKC) mfma_vgpr_fence(s);
     };
@@ -1005,7 +1181,11 @@ void mla_partial_kernel(PartialArgs a) {
     // so asking only for what is needed first lets the computation start
     // sooner.
     static_assert(kStages == 4, "prologue page ids");
+    static_assert(!F8 || TMLA_Q_LDS, "fp8 ring start-up stages Q through LDS");
     int pro_page[kStages] = {0, 0, 0, 0};
+    // fp8 cache: scales of sub-tiles i+1 (used by iteration i), i+2 and i+3
+    // (loading); scalar loads, rotated after the wait that completes them
+    float sc1 = 1.0f, sc2 = 1.0f, sc3 = 1.0f;
     if (PAGED && PAGE_UNIFORM) {
 #pragma unroll
       for (int i = 0; i < kStages; ++i) pro_page[i] = page_fetch(st0 + min(i, nst - 1));
@@ -1033,7 +1213,12 @@ void mla_partial_kernel(PartialArgs a) {
       // (wave 3: P buffer 0, written again only after the first barrier of
       // the loop), reads Q^T back with the K-operand offsets, and only then
       // are the rings handed to the KV copies.
-      const int qrope = s_owner ? (wave < kRopeStages ? OFF_R + wave * RSLOT : OFF_P) : 0;
+      // (fp8 cache: three V and two rope entries; wave 3's rows go to the
+      // staging area, and the rope rows of waves 2 and 3 to P buffer 0, which
+      // holds two rope entries when all four waves run S)
+      const int qv = wave < VST ? wave * VSLOT : OFF_S;
+      const int qrope = s_owner ? (wave < kRopeStages ? OFF_R + wave * RSLOT : OFF_P + (wave - kRopeStages) * RSLOT) : 0;
+      static_assert(!F8 || NHB < 4 || PSLOT >= 2 * RSLOT, "Q rope staging in P buffer 0");
       if (s_owner) {
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg) {
@@ -1042,7 +1227,7 @@ void mla_partial_kernel(PartialArgs a) {
                             ((lane & 7) ^ piece_swizzle(dma_r, rg)) * 16;
           static_for<NCB>([&](auto CB) __attribute__((always_inline)) {
             constexpr int cb = decltype(CB)::value;
-            char LDS_AS* dst = cb < NVB ? lds + wave * VSLOT + (rg * NVB + cb) * 1024
+            char LDS_AS* dst = cb < NVB ? lds + qv + (rg * NVB + cb) * 1024
                                         : lds + qrope + (rg * NRB + cb - NVB) * 1024;
             lds_copy16<cb * 128>(src, dst);
           });
@@ -1053,7 +1238,7 @@ void mla_partial_kernel(PartialArgs a) {
 #pragma unroll
         for (int kc = 0; kc < NKC; ++kc) {
           const int cb = kc >> 2;
-          const char LDS_AS* p = cb < NVB ? lds + wave * VSLOT + k_off_v[kc & 3] + cb * 1024
+          const char LDS_AS* p = cb < NVB ? lds + qv + k_off_v[kc & 3] + cb * 1024
                                           : lds + qrope - OFF_R + k_off_v[kc & 3] + k_rope_delta + (cb - NVB) * 1024;
           qop[kc] = *reinterpret_cast<const i16x8 LDS_AS*>(p);
         }
@@ -1061,12 +1246,29 @@ void mla_partial_kernel(PartialArgs a) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       lds_barrier();  // every wave has its Q^T before the rings are refilled
       pages_ready();
-      issue(st0, pro_page[0]);  // nst >= 1
-      if (nst > 1) {
-        issue(st0 + 1, pro_page[1]);
-        wait_vmcnt<LOADS>();
+      if constexpr (F8) {
+        // sub-tiles 0 and 1 into staging entries 0 and 1, their scales, and
+        // sub-tile 0 widened into ring entry 0 (the rings are free: every
+        // wave has its Q^T)
+        issue8(st0, pro_page[0]);  // nst >= 1
+        sc2 = s_load_f32(a.kv_scale + (int64_t)pro_page[0] * a.sc_s0);
+        sc3 = s_load_f32(a.kv_scale + (int64_t)pro_page[1] * a.sc_s0);
+        if (nst > 1) {
+          issue8(st0 + 1, pro_page[1]);
+          wait_vmcnt<LOADS8>();
+        } else {
+          wait_vmcnt<0>();
+        }
+        conv_read(0);
+        conv_write(0);
       } else {
-        wait_vmcnt<0>();
+        issue(st0, pro_page[0]);  // nst >= 1
+        if (nst > 1) {
+          issue(st0 + 1, pro_page[1]);
+          wait_vmcnt<LOADS>();
+        } else {
+          wait_vmcnt<0>();
+        }
       }
     } else if (TMLA_STARTUP == 0) {
       load_q();
@@ -1100,36 +1302,68 @@ void mla_partial_kernel(PartialArgs a) {
     // discarded. The body is instantiated twice: with the copies of sub-tile
     // i+3 (every iteration with i + 3 < nst, no per-copy condition) and
     // without them (the last three iterations).
-    static_assert(kStages == 4 && kRopeStages == 3, "ring offsets below");
+    static_assert(kStages == 4 && (F8 ? VST == 3 && kRopeStages == 2 : VST == 4 && kRopeStages == 3),
+                  "ring offsets below");
     auto iteration = [&](const int i, auto DOCOPY) __attribute__((always_inline)) {
       constexpr bool do_copy = decltype(DOCOPY)::value;  // sub-tile i+3
-      // sub-tile i+1 must have landed; sub-tile i+2 may still be in flight
-      if (do_copy) {  // here i + 2 < nst
-        if (i >= 0) wait_vmcnt<LOADS>();
-      } else if (i >= 0 && i + 1 < nst) {
-        if (i + 2 < nst) {
-          wait_vmcnt<LOADS>();
-        } else {
-          wait_vmcnt<0>();
+      int page = 0;
+      if constexpr (F8) {
+        // fp8: copy sub-tile i+3 into staging entry (i+3) & 1 (this wave
+        // widened its previous content, sub-tile i+1, in iteration i-1),
+        // fetch this wave's chunks of sub-tile i+2 (copied in iteration i-1),
+        // and once every wave is done with ring entries (i-1) % 3 (V) and
+        // i % 2 (rope) widen sub-tile i+2 into them
+        if (do_copy) {
+          page = page_ready(next_page);
+          issue8(st0 + i + 3, page);
         }
+        if (i + 2 < nst) {
+          if (do_copy) {
+            wait_vmcnt<LOADS8>();
+          } else {
+            wait_vmcnt<0>();
+          }
+          conv_read(i + 2);
+        }
+        // every wave's P^T(i) and factors are written; the scale of sub-tile
+        // i+2 has arrived
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(sc2), "+s"(sc3) : : "memory");
+        sc1 = sc2;
+        sc2 = sc3;
+        lds_barrier();
+        if (i + 2 < nst) conv_write(i + 2);
+      } else {
+        // sub-tile i+1 must have landed; sub-tile i+2 may still be in flight
+        if (do_copy) {  // here i + 2 < nst
+          if (i >= 0) wait_vmcnt<LOADS>();
+        } else if (i >= 0 && i + 1 < nst) {
+          if (i + 2 < nst) {
+            wait_vmcnt<LOADS>();
+          } else {
+            wait_vmcnt<0>();
+          }
+        }
+        page = (PAGED && PAGE_UNIFORM && do_copy) ? page_ready(next_page) : 0;
+        // every wave's P^T(i) and factors are written and every wave is done
+        // with the ring entries refilled during this iteration
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_barrier();
       }
-      const int page = (PAGED && PAGE_UNIFORM && do_copy) ? page_ready(next_page) : 0;
-      // every wave's P^T(i) and factors are written and every wave is done
-      // with the ring entries refilled during this iteration
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      lds_barrier();
-      // the page-id load goes out before every LDS read of the iteration, so
-      // its out-of-order return can only make the counted waits wait longer
+      // the page-id (and scale) loads go out before every counted LDS read of
+      // the iteration, so their out-of-order returns can only make the
+      // counted waits wait longer
       if (PAGED && PAGE_UNIFORM && i + kStages < nst)
         next_page = i < 0 ? pro_page[kStages - 1] : page_fetch(st0 + i + kStages);
+      if (F8 && do_copy) sc3 = s_load_f32(a.kv_scale + (int64_t)page * a.sc_s0);  // sub-tile i+3
       const int pbuf = i & 1;
       f32x4 alpha4 = ds_read_f32x4(lds + OFF_A + pbuf * ASLOT + (lane & 31) * 16);
       // ring entries (i + 1 >= 0): S(i+1) reads entry i+1, PV(i) entry i
-      // (entry 0 at i = -1, where P = 0), the copies fill entry i+3
+      // (entry 0 at i = -1, where P = 0), the copies fill entry i+3 (16-bit
+      // cache; the fp8 widening fills entry i+2 above)
       const unsigned k1 = (unsigned)(i + 1);
-      const unsigned r1 = k1 % 3u;
-      const char LDS_AS* vst = lds + (i < 0 ? 0u : (k1 + 3u) & 3u) * VSLOT;
-      const char LDS_AS* kst_v = lds + (k1 & 3u) * VSLOT;
+      const unsigned r1 = F8 ? (k1 & 1u) : k1 % 3u;
+      const char LDS_AS* vst = lds + (i < 0 ? 0u : (F8 ? (k1 + 2u) % 3u : (k1 + 3u) & 3u)) * VSLOT;
+      const char LDS_AS* kst_v = lds + (F8 ? k1 % 3u : k1 & 3u) * VSLOT;
       const char LDS_AS* kst_r = lds + r1 * RSLOT;
       const int copy_voff = (int)((k1 + 2u) & 3u) * VSLOT;
       const int copy_roff = (int)(r1 == 0u ? 2u : r1 - 1u) * RSLOT;
@@ -1149,7 +1383,7 @@ void mla_partial_kernel(PartialArgs a) {
         return [&](auto J) __attribute__((always_inline)) {
           constexpr int j = decltype(J)::value;
           constexpr int NST = decltype(NSTEPSC)::value;
-          if constexpr (j == 0 && do_copy) copy_src(st0 + i + kStages - 1, page, csrc);
+          if constexpr (j == 0 && do_copy && !F8) copy_src(st0 + i + kStages - 1, page, csrc);
           if constexpr (j == PV_START - 1) {
             pin_f4(alpha4);
             bool any = false;
@@ -1159,7 +1393,7 @@ void mla_partial_kernel(PartialArgs a) {
           }
           static_for<LOADS>([&](auto K) __attribute__((always_inline)) {
             constexpr int k = decltype(K)::value;
-            if constexpr (do_copy && k * NST / LOADS == j)
+            if constexpr (do_copy && !F8 && k * NST / LOADS == j)
               copy_one(copy_voff, copy_roff, k / NCB, std::integral_constant<int, k % NCB>{}, csrc);
           });
 
@@ -1182,7 +1416,14 @@ void mla_partial_kernel(PartialArgs a) {
         if (stamped) st_pass1 = stamp_now();
         // no token past the sequence (for the wave's earliest query token)
         const bool full = (st_s + 1) * kSubTokens <= n_b - lag_wave;
-        const float c = a.qk_scale_log2;
+        // (fp8 cache: the page's scale multiplies every score; a zero product
+        // runs as the smallest normal float of the same sign, as the host does
+        // for a zero softmax scale, so masked scores stay -inf)
+        float c = a.qk_scale_log2;
+        if constexpr (F8) {
+          c *= sc1;
+          if (c == 0.0f) c = copysignf(1.17549435e-38f, a.qk_scale_log2);
+        }
         float m_use = m_run, lsum = 0.0f, alpha = 1.0f;
         auto softmax_hook = [&](auto J) __attribute__((always_inline)) {
           constexpr int j = decltype(J)::value;
@@ -1223,6 +1464,10 @@ void mla_partial_kernel(PartialArgs a) {
             pin_f16(s);
             pin_f1(lsum);
           } else if constexpr (j == 2 + 16 / EXP_PER_STEP) {
+            if constexpr (F8) {  // the value product sees p times the page's scale
+#pragma unroll
+              for (int r = 0; r < 16; ++r) s[r] *= sc1;
+            }
             pack_probs_in_place<DT>(s);
           }
         };
@@ -1282,6 +1527,7 @@ void mla_partial_kernel(PartialArgs a) {
     for (; i < nst; ++i) iteration(i, std::false_type{});
     // every copy has landed and all waves are done with the rings before the
     // finalize reuses them
+    if constexpr (TMLA_MFMA_VOLATILE) mfma_agpr_fence(acc[NACC - 1]);  // the last PV MFMAs have landed
     wait_vmcnt<0>();
     lds_barrier();
     if (b == b_first) phase_stamp(3);
@@ -1606,9 +1852,9 @@ int check_common(const Common& c, const void* workspace, size_t ws_bytes) {
   return TMLA_OK;
 }
 
-template <int DT, int NHB, bool PAGED, bool UNI>
+template <int DT, int NHB, bool PAGED, bool UNI, bool F8 = false>
 hipError_t launch_partial_t(const PartialArgs& a, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((mla_partial_kernel<DT, 512, 64, NHB, PAGED, UNI>), grid, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((mla_partial_kernel<DT, 512, 64, NHB, PAGED, UNI, F8>), grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -1617,6 +1863,15 @@ hipError_t launch_partial_nw(const PartialArgs& a, dim3 grid, hipStream_t stream
   if (!paged) return launch_partial_t<DT, NHB, false, false>(a, grid, stream);
   if (uni) return launch_partial_t<DT, NHB, true, true>(a, grid, stream);
   return launch_partial_t<DT, NHB, true, false>(a, grid, stream);
+}
+
+// fp8 cache widened once per workgroup into the 16-bit ring (paged, pages
+// of whole sub-tiles, one scale per page or per tensor)
+template <int DT>
+hipError_t launch_partial_ring8(const PartialArgs& a, dim3 grid, int nhb, hipStream_t stream) {
+  if (nhb == 1) return launch_partial_t<DT, 1, true, true, true>(a, grid, stream);
+  if (nhb == 2) return launch_partial_t<DT, 2, true, true, true>(a, grid, stream);
+  return launch_partial_t<DT, 4, true, true, true>(a, grid, stream);
 }
 
 template <int DT>
@@ -1748,13 +2003,30 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   const int64_t cap_tokens = paged ? (int64_t)bt_cols * page_size : num_blocks;
   const size_t mid_o_bytes = wl.l - wl.o;  // partial rows, 256-byte aligned
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // one page per 32-token sub-tile (sub-tiles never straddle a page) and a
+  // power-of-two page size: page slots and in-page rows by shifts and masks
+  const bool uni = paged && (page_size % kSubTokens == 0) && a.page_shift >= 0;
   if (f8) {
-    // fp8 cache: groups of 16 heads, always two launches (no in-kernel merge)
+    // fp8 cache, always two launches (no in-kernel merge). More than
+    // kFp8GroupHeads heads with one scale per page (or per tensor) and pages
+    // of whole sub-tiles: the 16-bit kernel with the cache widened once per
+    // workgroup into its ring; otherwise groups of 16 heads, each streaming
+    // and widening the cache on its own.
     a.kv_scale = f8->scale;
     a.sc_s0 = f8->s0;
     a.sc_s1 = f8->s1;
-    const dim3 grid(worker_grid(batch, num_splits, num_workers, cap_tokens), (num_heads + 15) / 16);
-    hipError_t e = launch_partial_fp8(a, grid, dtype, paged, s);
+    hipError_t e;
+    if (uni && f8->s1 == 0 && num_heads > kFp8GroupHeads) {
+      const LaunchPlan plan = plan_launch(batch, num_heads, num_splits, num_workers, cap_tokens, mid_o_bytes,
+                                          mode == 0 ? 0 : 2, current_cu_count());
+      a.fused = 0;
+      e = dtype == TMLA_BF16 ? launch_partial_ring8<TMLA_BF16>(a, plan.grid, plan.nhb, s)
+                             : launch_partial_ring8<TMLA_FP16>(a, plan.grid, plan.nhb, s);
+      if (e != hipSuccess) return hip_fail(e, "mla_partial_kernel (fp8 ring) launch");
+    } else {
+      const dim3 grid(worker_grid(batch, num_splits, num_workers, cap_tokens), (num_heads + 15) / 16);
+      e = launch_partial_fp8(a, grid, dtype, paged, s);
+    }
     if (e != hipSuccess) return hip_fail(e, "mla_partial_fp8_kernel launch");
     if (mode != 0)
       return tmla_mla_decode_combine(seqlens, batch, num_heads, head_dim_v, dtype, num_splits, num_workers, out,
@@ -1767,9 +2039,6 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   const dim3 grid = plan.grid;
   a.mid_o_bytes = (int32_t)(mid_o_bytes < (size_t)INT32_MAX ? mid_o_bytes : 0);
   a.fused = plan.fused ? 1 : 0;
-  // one page per 32-token sub-tile (sub-tiles never straddle a page) and a
-  // power-of-two page size: page slots and in-page rows by shifts and masks
-  const bool uni = paged && (page_size % kSubTokens == 0) && a.page_shift >= 0;
   hipError_t e = dtype == TMLA_BF16 ? launch_partial_dt<TMLA_BF16>(a, grid, nhb, s, paged, uni)
                                     : launch_partial_dt<TMLA_FP16>(a, grid, nhb, s, paged, uni);
   if (e != hipSuccess) return hip_fail(e, "mla_partial_kernel launch");
