@@ -21,8 +21,9 @@ beside it with min / median / p90. After the timed region, the public
 host-side argument checks included) is timed the way the reference's bench
 times it.
 
-Then the fp8-cache leg (``fp8_cache`` in the JSON line; ``--no-fp8`` skips
-it): the 16-head ragged workload (B=64, 1K..32K tokens, page 64) with its
+Then the fp8-cache legs (``fp8_cache`` and ``fp8_cache_h128`` in the JSON
+line; ``--no-fp8`` skips them): the 16-head ragged workload (B=64, 1K..32K
+tokens, page 64) and the measured 128-head workload above, each with its
 cache quantised to E4M3 with one float32 scale per page, timed interleaved
 with the bf16 decode of the unquantised cache (two-kernel steps and partial
 kernels alone), with the fp8 partial kernel's roofline over the fp8 bytes.
@@ -111,17 +112,15 @@ def cpu_baseline(inp, target_s):
             "out_ref": out_ref}
 
 
-def fp8_leg(args, dev, flush, stream):
-    """The fp8 (E4M3, one scale per page) cache on the 16-head ragged
-    workload (B=64, 1K..32K tokens, page 64): the two-kernel step and the
-    partial kernel alone, interleaved with the bf16 decode of the same
-    cache before quantisation."""
+def fp8_leg(args, dev, flush, stream, host, kernel):
+    """The fp8 (E4M3, one scale per page) cache on one workload: the
+    two-kernel step and the partial kernel alone, interleaved with the bf16
+    decode of the same cache before quantisation."""
     import torch
 
-    from triton_mla import quantize_kv_fp8, workloads
+    from triton_mla import quantize_kv_fp8
     from triton_mla.kernel import DecodeLaunch
 
-    host = workloads.ragged_b64_h16()
     g = host.to(dev)
     codes, scale = quantize_kv_fp8(g.kv_cache, "page")
     c8 = DecodeLaunch(g.q, codes, g.seqlens, g.block_table, 512, host.softmax_scale, None, kv_scale=scale)
@@ -157,7 +156,7 @@ def fp8_leg(args, dev, flush, stream):
         "workload": host.name, "batch": host.batch, "heads": host.heads, "tokens": tokens, "page_size": 64,
         "format": "e4m3 codes + float32 scale per page", "algorithmic_bytes": bytes8,
         "step_us": {k: spread(v) for k, v in us.items()},
-        "roofline": {"bound": "hbm", "kernel": "mla_partial_fp8_kernel", "partial_us_mean": round(p8, 2),
+        "roofline": {"bound": "hbm", "kernel": kernel, "partial_us_mean": round(p8, 2),
                      "achieved": round(bytes8 / (p8 * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(bytes8 / (p8 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "step_frac": round(bytes8 / (med["fp8_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
@@ -278,7 +277,13 @@ def main():
     except RuntimeError as exc:  # capture unsupported in this environment
         print(f"graph capture failed: {exc}", file=sys.stderr)
 
-    fp8 = None if args.no_fp8 else fp8_leg(args, dev, flush, stream)
+    fp8 = {}
+    if not args.no_fp8:
+        # 16 heads: the 16-head-group kernel; 128 heads: the 16-bit kernel
+        # with the cache widened once per workgroup into its ring
+        fp8["fp8_cache"] = fp8_leg(args, dev, flush, stream, workloads.ragged_b64_h16(), "mla_partial_fp8_kernel")
+        fp8["fp8_cache_h128"] = fp8_leg(args, dev, flush, stream, workloads.b32_h128_8k(),
+                                        "mla_partial_kernel (fp8 cache widened into the ring)")
 
     if args.copy_mib > 0:
         src = torch.ones(args.copy_mib << 18, dtype=torch.int32, device=dev)
@@ -333,8 +338,8 @@ def main():
         "timed_launches": {k: args.steps for k in us},
         "graph_replay_matches_eager": graph_ok,
     }
-    if fp8 is not None:
-        result["fp8_cache"] = fp8["summary"]
+    for key, leg in fp8.items():
+        result[key] = leg["summary"]
 
     if not args.no_cpu_baseline:
         import numpy as np
@@ -371,16 +376,16 @@ def main():
         if cb["out_ref"] is not None:
             result["cpu_baseline"]["gpu_vs_cpu_ref_max_abs_err"] = \
                 (eager_out.float().cpu() - cb["out_ref"].float()).abs().max().item()
-        if fp8 is not None:
-            # the fp8 leg's gate: the float64 fp8 oracle on its first two sequences
-            f = fp8["gate"]
+        for key, leg in fp8.items():
+            # the fp8 legs' gates: the float64 fp8 oracle on their first two sequences
+            f = leg["gate"]
             ref8, _ = oracle.mla_decode_fp8_ref(u16(f["q"][:n]), f["codes"], f["scale"], f["seqlens"][:n],
                                                 f["bt"][:n], 512, f["softmax_scale"])
             err8 = (f["out"][:n].float() - torch.from_numpy(ref8)).abs().max().item()
             if not err8 <= 1e-2:
-                print(f"fp8 correctness gate failed: max |gpu - oracle| = {err8}", file=sys.stderr)
+                print(f"{key} correctness gate failed: max |gpu - oracle| = {err8}", file=sys.stderr)
                 sys.exit(1)
-            result["fp8_cache"]["gpu_vs_oracle_max_abs_err"] = err8
+            result[key]["gpu_vs_oracle_max_abs_err"] = err8
     print(json.dumps(result), flush=True)
 
 

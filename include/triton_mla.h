@@ -237,6 +237,10 @@ int tmla_mla_decode_causal(const void* q, int64_t q_stride_b, int64_t q_stride_h
  * the row's scale rounded to dtype for the value product, float32
  * accumulation. The workspace is tmla_workspace_bytes(batch, q_len *
  * num_heads, ...); the partials use tmla_mla_decode_combine's format.
+ * With more than 16 (virtual) heads, one scale per page or per tensor
+ * (scale_stride_1 = 0) and pages of a power-of-two multiple of 32 tokens, the
+ * cache is widened once per workgroup into the 16-bit kernel's ring; other
+ * calls run groups of 16 heads that each stream the cache.
  */
 int tmla_mla_decode_fp8(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
                         int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
