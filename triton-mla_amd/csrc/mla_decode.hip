@@ -774,6 +774,33 @@ void mla_partial_kernel(PartialArgs a) {
   // the last (record 1) segment of the worker's range; b < 0 = none
   if (a.fused && tid == 0) s_pend[0][0] = s_pend[1][0] = -1;
 
+  // Q rows of sequence bq for this wave's heads into LDS (the KV copies'
+  // swizzled layout; heads past num_heads copy head 0's row): V part at qv,
+  // rope part at qrope. The 16-bit cache stages wave w in V ring entry w and
+  // rope entry w (wave 3: P buffer 0, written again only after the first
+  // barrier of the loop); the fp8 ring (three V and two rope entries) stages
+  // wave 3's rows in the staging area and the rope rows of waves 2 and 3 in P
+  // buffer 0, which holds two rope entries when all four waves run S.
+  const int qv = wave < VST ? wave * VSLOT : OFF_S;
+  const int qrope = s_owner ? (wave < kRopeStages ? OFF_R + wave * RSLOT : OFF_P + (wave - kRopeStages) * RSLOT) : 0;
+  static_assert(!F8 || NHB < 4 || PSLOT >= 2 * RSLOT, "Q rope staging in P buffer 0");
+  auto stage_q = [&](int bq) __attribute__((always_inline)) {
+    const int ln = lane_id_fresh();
+    const int r = ln >> 3;
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const int hq = head_base + 8 * rg + r;
+      const char* src = a.q + ((int64_t)bq * a.q_sb + (int64_t)(hq < a.num_heads ? hq : 0) * a.q_sh) * 2 +
+                        ((ln & 7) ^ piece_swizzle(r, rg)) * 16;
+      static_for<NCB>([&](auto CB) __attribute__((always_inline)) {
+        constexpr int cb = decltype(CB)::value;
+        char LDS_AS* dst = cb < NVB ? lds + qv + (rg * NVB + cb) * 1024
+                                    : lds + qrope + (rg * NRB + cb - NVB) * 1024;
+        lds_copy16<cb * 128>(src, dst);
+      });
+    }
+  };
+
   // ---- work range -------------------------------------------------------
   WorkRange wr;
   if (!work_range(a, worker, wr)) {
@@ -1213,26 +1240,7 @@ void mla_partial_kernel(PartialArgs a) {
       // (wave 3: P buffer 0, written again only after the first barrier of
       // the loop), reads Q^T back with the K-operand offsets, and only then
       // are the rings handed to the KV copies.
-      // (fp8 cache: three V and two rope entries; wave 3's rows go to the
-      // staging area, and the rope rows of waves 2 and 3 to P buffer 0, which
-      // holds two rope entries when all four waves run S)
-      const int qv = wave < VST ? wave * VSLOT : OFF_S;
-      const int qrope = s_owner ? (wave < kRopeStages ? OFF_R + wave * RSLOT : OFF_P + (wave - kRopeStages) * RSLOT) : 0;
-      static_assert(!F8 || NHB < 4 || PSLOT >= 2 * RSLOT, "Q rope staging in P buffer 0");
-      if (s_owner) {
-#pragma unroll
-        for (int rg = 0; rg < 4; ++rg) {
-          const int hq = head_base + 8 * rg + dma_r;
-          const char* src = a.q + ((int64_t)b * a.q_sb + (int64_t)(hq < a.num_heads ? hq : 0) * a.q_sh) * 2 +
-                            ((lane & 7) ^ piece_swizzle(dma_r, rg)) * 16;
-          static_for<NCB>([&](auto CB) __attribute__((always_inline)) {
-            constexpr int cb = decltype(CB)::value;
-            char LDS_AS* dst = cb < NVB ? lds + qv + (rg * NVB + cb) * 1024
-                                        : lds + qrope + (rg * NRB + cb - NVB) * 1024;
-            lds_copy16<cb * 128>(src, dst);
-          });
-        }
-      }
+      if (s_owner) stage_q(b);
       wait_vmcnt<0>();
       if (s_owner) {
 #pragma unroll
