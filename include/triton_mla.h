@@ -279,8 +279,8 @@ int32_t tmla_device_cu_count(int32_t device);
 
 /*
  * MLA layer glue: the absorbed-projection steps on either side of
- * tmla_mla_decode in one decode step of the DeepSeek MLA layer. The dense
- * projections (wq_a, wq_b, wkv_a, wo) stay library GEMMs. wkv_b is the
+ * tmla_mla_decode in one decode step of the DeepSeek MLA layer, and the
+ * dense projections (wq_a, wq_b, wkv_a, wo) of a step's few rows. wkv_b is the
  * layer's [num_heads * (qk_nope_dim + v_head_dim), kv_lora_rank] weight with
  * row stride wkv_b_stride_0: rows h*(nope+v) .. +nope are W_UK[h], the next v
  * rows W_UV[h] (the reference's view, src/triton_mla/model.py:96-99).
@@ -339,6 +339,44 @@ int tmla_mla_kv_append(const void* kv_proj, int64_t kv_proj_stride_b, const void
                        int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks,
                        int32_t page_size, const int32_t* block_table, int64_t bt_stride_b,
                        int32_t bt_cols, void* stream);
+
+/*
+ * RMSNorm of rows: y[r, :] = x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * weight
+ * in float32 (the normalised value times the weight), rounded once to the
+ * dtype. Replaces `RMSNorm.forward` (src/triton_mla/model.py:34-41) on the
+ * query latent of `MLA._project` (model.py:76). weight [dim] may be NULL
+ * (weight 1). Row strides in elements, multiples of 8; x, weight and y
+ * 16-byte aligned; built for dim a multiple of 8.
+ */
+int tmla_mla_rms_norm(const void* x, int64_t x_stride, const void* weight, float eps, int32_t rows,
+                      int32_t dim, int32_t dtype, void* y, int64_t y_stride, void* stream);
+
+/*
+ * Dense projection of a decode step's rows: y[m, n] = x[m, :] . w[n, :]
+ * (float32 accumulation, rounded once to the dtype), i.e. nn.Linear without
+ * bias with w in its [out_features, in_features] layout. Replaces the
+ * library GEMMs of the four projections of `MLA.forward` / `MLA._project`
+ * (src/triton_mla/model.py:66-72 define them; model.py:74-82, 124 apply
+ * them) for batches of at most 64 rows, where a GEMM library's tiles leave
+ * most compute units idle: every weight row is read once, by workgroups of
+ * 64 (or 16) output columns, and the contraction is split over the waves of
+ * a workgroup and, when there are few column groups, over several
+ * workgroups, whose tiles are summed in a fixed order, so the result does
+ * not depend on timing. Row strides in elements; x and w 16-byte aligned
+ * with row strides a multiple of 8. Built for m <= 64, n a multiple of 16
+ * and k a multiple of 64 (TMLA_ERR_UNSUPPORTED otherwise).
+ *
+ * workspace: tmla_mla_project_workspace_bytes(m, n, k) bytes, 256-byte
+ * aligned (may be NULL when that is 0), zero-filled before its first use:
+ * a fixed 64 KiB block of arrival counters, then the partial tiles of a
+ * split contraction. Every call leaves its counters at zero again, so one
+ * buffer at least as large as each call's need serves calls of any shapes
+ * in turn. Calls that share a workspace must not run concurrently.
+ */
+size_t tmla_mla_project_workspace_bytes(int32_t m, int32_t n, int32_t k);
+int tmla_mla_project(const void* x, int64_t x_stride, const void* w, int64_t w_stride, int32_t m,
+                     int32_t n, int32_t k, int32_t dtype, void* y, int64_t y_stride, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

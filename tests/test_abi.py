@@ -134,6 +134,42 @@ def test_layer_glue_arguments_rejected_on_host(lib):
     assert lib.tmla_mla_kv_append(*args) == 1 and b"page_size" in lib.tmla_last_error()
     args = list(k); args[13] = 0
     assert lib.tmla_mla_kv_append(*args) == 1
+    # tmla_mla_rms_norm(x, x_s, w, eps, rows, dim, dtype, y, y_s, stream)
+    rn = [fake, 1536, fake, 1e-6, 16, 1536, 0, fake, 1536, None]
+    args = list(rn); args[5] = 1540; args[1] = 1544; args[8] = 1544
+    assert lib.tmla_mla_rms_norm(*args) == 2  # dim not a multiple of 8
+    args = list(rn); args[7] = None
+    assert lib.tmla_mla_rms_norm(*args) == 1 and b"null" in lib.tmla_last_error()
+    args = list(rn); args[2] = ctypes.c_void_p((1 << 20) + 4)
+    assert lib.tmla_mla_rms_norm(*args) == 1 and b"aligned" in lib.tmla_last_error()
+    args = list(rn); args[1] = 1532
+    assert lib.tmla_mla_rms_norm(*args) == 1  # row stride below dim
+    args = list(rn); args[4] = 0
+    assert lib.tmla_mla_rms_norm(*args) == 0  # no rows: nothing to do
+    # tmla_mla_project(x, x_s, w, w_s, m, n, k, dtype, y, y_s, workspace, workspace_bytes, stream)
+    need = lib.tmla_mla_project_workspace_bytes(16, 1536, 7168)
+    assert need > 0 and lib.tmla_mla_project_workspace_bytes(65, 1536, 7168) == 0
+    pr = [fake, 7168, fake, 7168, 16, 1536, 7168, 0, fake, 1536, fake, need, None]
+    args = list(pr); args[4] = 65
+    assert lib.tmla_mla_project(*args) == 2  # more than 64 rows
+    args = list(pr); args[5] = 1544
+    assert lib.tmla_mla_project(*args) == 2  # n not a multiple of 16
+    args = list(pr); args[6] = 7144; args[1] = 7144; args[3] = 7144
+    assert lib.tmla_mla_project(*args) == 2  # k not a multiple of 64 (nor of 32)
+    args = list(pr); args[7] = 7
+    assert lib.tmla_mla_project(*args) == 1 and b"dtype" in lib.tmla_last_error()
+    args = list(pr); args[2] = None
+    assert lib.tmla_mla_project(*args) == 1 and b"null" in lib.tmla_last_error()
+    args = list(pr); args[0] = ctypes.c_void_p((1 << 20) + 8)
+    assert lib.tmla_mla_project(*args) == 1 and b"aligned" in lib.tmla_last_error()
+    args = list(pr); args[1] = 7164
+    assert lib.tmla_mla_project(*args) == 1  # row stride not a multiple of 8 (and < k)
+    args = list(pr); args[11] = need - 256
+    assert lib.tmla_mla_project(*args) == 3  # workspace too small
+    args = list(pr); args[10] = None
+    assert lib.tmla_mla_project(*args) == 3  # workspace missing
+    args = list(pr); args[4] = 0
+    assert lib.tmla_mla_project(*args) == 0  # no rows: nothing to do
 
 
 def test_noalloc_rejects_calls_beyond_the_scratch(lib):

@@ -163,6 +163,128 @@ def test_absorb_out_matches_oracle(gpu, batch, heads):
     assert_matches(bits(out.cpu()), ref, dot_bound(rank, abs_sum), f"o . W_UV (B={batch}, H={heads})")
 
 
+@pytest.mark.parametrize("rows,dim,strided", [(16, 1536, True), (3, 512, False), (9, 4104, False)])
+def test_rms_norm_matches_oracle(gpu, rows, dim, strided):
+    """RMSNorm of rows (tmla_mla_rms_norm) against the float64 oracle's
+    rms_norm: within half a bf16 ulp plus the float32 error of the sum of
+    squares, the rsqrt and two products ((dim + 8) * 2^-24 relative)."""
+    from triton_mla import layer_ops
+
+    gen = torch.Generator().manual_seed(rows * 31 + dim)
+    width = dim + (64 if strided else 0)
+    xbuf = (2.0 * torch.randn(rows, width, generator=gen)).to(torch.bfloat16)
+    w = (1.0 + 0.3 * torch.randn(dim, generator=gen)).to(torch.bfloat16)
+    xg = xbuf.to(gpu)[:, :dim]
+    y = layer_ops.rms_norm(xg, w.to(gpu), 1e-6)
+    torch.cuda.synchronize(gpu)
+    ref = oracle.rms_norm(f64(xbuf[:, :dim]), f64(w), 1e-6)
+    assert_matches(bits(y.cpu()), ref, np.abs(ref) * (dim + 8) * 2.0 ** -24, f"rms_norm ({rows}x{dim})")
+
+
+# (m, n, k): the four DeepSeek-V3 projections of a 16-row step (wq_a, wq_b,
+# wkv_a, wo), then row counts of 1 to 64 (one to four 16-row blocks, partial
+# blocks), 16-column groups (n not a multiple of 64), contractions of one
+# 64-element chunk, fewer chunks than waves, and chunk counts that split
+# unevenly over waves and workgroups
+PROJECT_SHAPES = [(16, 1536, 7168), (16, 24576, 1536), (16, 576, 7168), (16, 7168, 16384),
+                  (1, 64, 128), (5, 48, 1024), (33, 32, 320), (64, 16, 64), (17, 80, 4032),
+                  (48, 112, 2112), (2, 4096, 64 * 37)]
+
+
+@pytest.mark.parametrize("m,n,k", PROJECT_SHAPES)
+def test_project_matches_oracle(gpu, m, n, k):
+    """y = x . W^T (tmla_mla_project) against the float64 product: within half a
+    bf16 ulp plus the float32 bound of a k-term dot product, elementwise;
+    at least 99% correctly rounded (a float32 sum lands on the other side of
+    a rounding boundary for about 2^-8 of the elements at k = 16K)."""
+    from triton_mla import layer_ops
+
+    gen = torch.Generator().manual_seed(m * 7919 + n * 31 + k)
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16)
+    w = (0.02 * torch.randn(n, k, generator=gen)).to(torch.bfloat16)
+    xg, wg = x.to(gpu), w.to(gpu)
+    assert layer_ops.project_fits(xg, wg)
+    y = layer_ops.project(xg, wg)
+    again = [layer_ops.project(xg, wg) for _ in range(5)]
+    torch.cuda.synchronize(gpu)
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    for i, y2 in enumerate(again):
+        assert np.array_equal(bits(y.cpu()), bits(y2.cpu())), f"call {i + 1} differs from the first"
+    ref = f64(x) @ f64(w).T
+    abs_sum = np.abs(f64(x)) @ np.abs(f64(w)).T
+    assert_matches(bits(y.cpu()), ref, dot_bound(k, abs_sum), f"x . W^T ({m}x{n}x{k})", min_exact=0.99)
+
+
+def test_project_workspace_shared_across_shapes(gpu):
+    """Calls of different shapes in turn on one workspace, zero-filled once:
+    a narrow weight (many split-contraction tiles, few counters) and a wide
+    one (fewer tiles, more counters) give the bits of a call on a fresh
+    workspace, every time."""
+    from triton_mla import _native
+
+    lib = _native.load()
+    gen = torch.Generator().manual_seed(5)
+    shapes = [(16, 1536, 7168), (16, 7168, 16384), (3, 576, 7168)]
+    data = []
+    for m, n, k in shapes:
+        x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(gpu)
+        w = (0.02 * torch.randn(n, k, generator=gen)).to(torch.bfloat16).to(gpu)
+        data.append((x, w))
+    need = max(lib.tmla_mla_project_workspace_bytes(m, n, k) for m, n, k in shapes)
+    shared = torch.zeros(need, dtype=torch.uint8, device=gpu)
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+
+    def call(i, ws):
+        x, w = data[i]
+        m, n, k = shapes[i]
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+        with torch.cuda.device(gpu):
+            _native.check(lib.tmla_mla_project(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), m, n, k,
+                                               _native.DTYPE_CODE[torch.bfloat16], y.data_ptr(), y.stride(0),
+                                               ws.data_ptr(), ws.numel(), stream), "tmla_mla_project")
+        return y
+
+    fresh = []
+    for i in range(len(shapes)):
+        ws = torch.zeros(max(lib.tmla_mla_project_workspace_bytes(*shapes[i]), 256), dtype=torch.uint8, device=gpu)
+        fresh.append(call(i, ws))
+        torch.cuda.synchronize(gpu)
+    for rep in range(3):
+        for i in (0, 1, 2, 1, 0):
+            y = call(i, shared)
+            torch.cuda.synchronize(gpu)
+            assert torch.equal(y, fresh[i]), f"shape {shapes[i]} differs on the shared workspace (round {rep})"
+
+
+def test_project_fp16_and_strided_rows(gpu):
+    """fp16 operands, and x / y rows inside wider buffers (row strides larger
+    than the row): same product, other rows of the output buffer untouched."""
+    from triton_mla import layer_ops, _native
+
+    gen = torch.Generator().manual_seed(99)
+    m, n, k = 9, 64, 640
+    xbuf = torch.randn(m, k + 64, generator=gen).to(torch.float16)
+    w = (0.05 * torch.randn(n, k, generator=gen)).to(torch.float16)
+    xg, wg = xbuf.to(gpu)[:, :k], w.to(gpu)
+    assert xg.stride(0) == k + 64 and layer_ops.project_fits(xg, wg)
+    ybuf = torch.full((m, n + 16), 7.0, dtype=torch.float16, device=gpu)
+    lib = _native.load()
+    need = lib.tmla_mla_project_workspace_bytes(m, n, k)
+    ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=gpu)
+    with torch.cuda.device(gpu):
+        _native.check(lib.tmla_mla_project(xg.data_ptr(), xg.stride(0), wg.data_ptr(), wg.stride(0), m, n, k,
+                                           _native.DTYPE_CODE[torch.float16], ybuf.data_ptr(), ybuf.stride(0),
+                                           ws.data_ptr(), ws.numel(), torch.cuda.current_stream(gpu).cuda_stream),
+                      "tmla_mla_project")
+    torch.cuda.synchronize(gpu)
+    got = ybuf[:, :n].double().cpu().numpy()
+    ref = f64(xbuf[:, :k]) @ f64(w).T
+    abs_sum = np.abs(f64(xbuf[:, :k])) @ np.abs(f64(w)).T
+    fp16_half_ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -14))) - 11)
+    assert np.all(np.abs(got - ref) <= fp16_half_ulp + dot_bound(k, abs_sum)), "fp16 product off"
+    assert bool((ybuf[:, n:] == 7.0).all()), "columns past n written"
+
+
 def test_hip_glue_matches_torch_glue(gpu):
     """The absorbed step with the HIP glue and with the reference's torch glue
     (same mla_decode inside) on the same inputs: the appended rows agree to
@@ -191,3 +313,35 @@ def test_hip_glue_matches_torch_glue(gpu):
     ulp = torch.from_numpy(ulp_bf16(cb.float().cpu().numpy().astype(np.float64))).to(gpu)
     assert bool((diff <= ulp).all()), "appended rows differ by more than one bf16 ulp"
     torch.testing.assert_close(out_hip.float(), out_torch.float(), atol=3e-2, rtol=3e-2)
+
+
+def test_layer_step_graph_replays(gpu):
+    """MLA.forward captured in a graph (the serving form of the decode step:
+    no host work between its kernels) replays to the eager step's bits, three
+    times, with eager steps in between."""
+    from triton_mla import MLA, MLAConfig
+    from triton_mla.bench import capture_layer_step
+
+    gen = torch.Generator().manual_seed(21)
+    cfg = MLAConfig(hidden_size=512, num_heads=32, q_lora_rank=256)
+    model = MLA(cfg)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_(torch.randn(p.shape, generator=gen) * 0.05)
+    model = model.to(gpu, torch.bfloat16)
+    batch, page, pages = 4, 64, 6
+    seqlens = torch.tensor([5, 64, 200, 321], dtype=torch.int32, device=gpu)
+    bt = torch.randperm(batch * pages, generator=gen).view(batch, pages).int().to(gpu)
+    cache = torch.randn(batch * pages, page, cfg.kv_cache_dim, generator=gen).to(gpu, torch.bfloat16)
+    x = torch.randn(batch, cfg.hidden_size, generator=gen).to(gpu, torch.bfloat16)
+    with torch.no_grad():
+        eager, _ = model(x, cache, seqlens, bt)
+        eager = eager.clone()
+        graph, out = capture_layer_step(model, x, cache, seqlens, bt, gpu)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize(gpu)
+            assert torch.equal(out, eager), "graph replay differs from the eager step"
+            again, _ = model(x, cache, seqlens, bt)  # eager work between replays
+            torch.cuda.synchronize(gpu)
+            assert torch.equal(again, eager)

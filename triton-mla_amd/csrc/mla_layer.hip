@@ -5,7 +5,8 @@
 // Reference behaviour: src/triton_mla/model.py:74-124 (MLA._project's RoPE,
 // MLA._append_kv, the W_UK and W_UV einsums of MLA.forward), apply_rope
 // model.py:44-50, RMSNorm model.py:34-41. The dense projections (wq_a, wq_b,
-// wkv_a, wo) stay library GEMMs.
+// wkv_a, wo) of a decode step's few rows run in mla_project_kernel; larger
+// batches stay library GEMMs.
 //
 //  * mla_absorb_q_kernel: q[b, h, :rank] = q_nope[b, h] . W_UK[h] and
 //    q[b, h, rank:] = RoPE(q_pe[b, h]). W_UK[h] (the nope rows of wkv_b,
@@ -22,6 +23,13 @@
 //    memory; four waves split the contraction of each 32 x 32 block.
 //  * mla_kv_append_kernel: RMSNorm of the latent, RoPE of the key, and the
 //    new row written at position cache_seqlens[b] through the block table.
+//  * mla_rms_norm_kernel: RMSNorm of rows (the query latent, model.py:34-41,
+//    76), float32, rounded once.
+//  * mla_project_kernel: the dense projections (wq_a, wq_b, wkv_a, wo;
+//    nn.Linear, model.py:66-72) for a decode step's few rows,
+//    y[M, N] = x[M, K] . W[N, K]^T: each weight row is read from HBM once,
+//    16 rows per workgroup, the contraction split over the workgroup's
+//    waves and summed through LDS in a fixed order.
 #include <math.h>
 #include <stdio.h>
 
@@ -36,6 +44,7 @@ constexpr int kNope = 128;   // qk_nope_head_dim the q kernel is built for
 constexpr int kRope = 64;    // qk_rope_head_dim
 constexpr int kColsWG = 128; // W_UK columns per workgroup (4 waves x 1 block of 32)
 constexpr int kBTile = 32;   // batch rows per MFMA block (N of the 32x32x16 MFMA)
+constexpr int kProjectMaxRows = 64;  // rows of x the projection kernel takes (4 blocks of 16)
 
 struct AbsorbQArgs {
   const short* qp;       // [B, qp_sb]: head h at h*(nope+rope): q_nope then q_pe
@@ -72,6 +81,18 @@ struct KvAppendArgs {
   const int32_t* bt;     // [B, bt_cols] or null (dense)
   int64_t bt_sb;
   int32_t bt_cols, batch, rank;
+};
+
+struct ProjectArgs {
+  const short* x;        // [M, K], row stride x_s (elements)
+  int64_t x_s;
+  const short* w;        // [N, K] (nn.Linear weight), row stride w_s
+  int64_t w_s;
+  short* y;              // [M, N], row stride y_s
+  int64_t y_s;
+  float* ws;             // partial tiles of split contractions (KS > 1)
+  int32_t* cnt;          // their arrival counters, one per column group
+  int32_t m, n, k;
 };
 
 // RoPE of one rotation pair (x1 = element i, x2 = element i + dim/2) at
@@ -303,6 +324,279 @@ __global__ __launch_bounds__(256) void mla_kv_append_kernel(KvAppendArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// RMSNorm of rows (the query latent): grid (cdiv(rows, 4)), one wave per row
+// ---------------------------------------------------------------------------
+struct RmsNormArgs {
+  const short* x;
+  int64_t x_s;
+  const short* w;        // [dim] or null (weight 1)
+  short* y;
+  int64_t y_s;
+  float eps;
+  int32_t rows, dim;
+};
+
+// y = x * rsqrt(mean(x^2) + eps) * weight in float32, rounded once (the
+// arithmetic of the latent's norm in mla_kv_append_kernel). Lane l owns the
+// 8-element chunks l, l + 64, ...; the row is read twice (the second pass
+// from cache).
+template <int DT>
+__global__ __launch_bounds__(256) void mla_rms_norm_kernel(RmsNormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;  // wave-uniform
+  const short* x = a.x + (int64_t)row * a.x_s;
+  const int chunks = a.dim / 8;
+  float ss = 0.0f;
+  for (int j = lane; j < chunks; j += 64) {
+    const i16x8 v = *reinterpret_cast<const i16x8*>(x + 8 * j);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = Elt<DT>::to_float(v[e]);
+      ss += f * f;
+    }
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
+  const float rstd = rsqrtf(ss / (float)a.dim + a.eps);
+  short* y = a.y + (int64_t)row * a.y_s;
+  for (int j = lane; j < chunks; j += 64) {
+    const i16x8 v = *reinterpret_cast<const i16x8*>(x + 8 * j);
+    i16x8 w8 = (i16x8)0;
+    if (a.w) w8 = *reinterpret_cast<const i16x8*>(a.w + 8 * j);
+    i16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float f = Elt<DT>::to_float(v[e]) * rstd;
+      if (a.w) f = f * Elt<DT>::to_float(w8[e]);
+      o[e] = Elt<DT>::from_float(f);
+    }
+    *reinterpret_cast<i16x8*>(y + 8 * j) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dense projection: grid (N / (16 CB), KS), 4 waves; y rows in MB blocks of 16
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(i16x8 a, i16x8 b, f32x4 c) {
+  if constexpr (DT == TMLA_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+}
+
+// Partial tiles are exchanged between the workgroups of one column group
+// through memory within the launch: written through to memory (sc0 sc1),
+// counted with a system-scope atomic, read back with loads that bypass the
+// caches (sc0 sc1), so no cache maintenance is needed between workgroups on
+// different XCDs.
+__device__ __forceinline__ void store_through16(void* p, f32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
+}
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource word 3 (32-bit data format)
+constexpr int kSysCoherent = 1 | 16;      // sc0 | sc1
+
+// Workgroup = output columns [16 CB * blockIdx.x, +16 CB) over chunks (64
+// contraction elements, 128 bytes of a weight row) [ks * C / KS,
+// (ks + 1) * C / KS) of the C = K / 64, ks = blockIdx.y; its 4 waves split
+// that range evenly. Each wave streams its chunks of the group's weight rows
+// into its own LDS slots with LDS-DMA (8 rows x 128 bytes per copy: whole
+// cache lines, one chunk ahead of its MFMAs), so no barrier is needed, and
+// reads them back as MFMA operands. v_mfma_f32_16x16x32: A = x rows (lane:
+// row lane % 16), B = W rows (lane: column lane % 16), D lane: column
+// lane % 16, rows 4 * (lane / 16) .. +4; k-step s of a chunk gives lane
+// group q = lane / 16 the elements 8 * (4 s + q) .. +8 of the chunk (the
+// same for x and W). The 16-byte piece p of row r of an 8-row block sits at
+// p ^ r, which keeps both the copies (one row per 8 lanes) and the operand
+// reads (16 rows, one piece each) free of bank conflicts. x costs MB KiB per
+// k-step from L2 against CB KiB of weights. The waves' tiles are summed in
+// LDS in wave order; with KS > 1 each workgroup stores its tile to the
+// workspace and the last of the column group's KS workgroups to arrive sums
+// the KS tiles in ks order, writes y and resets the group's counter, so the
+// result does not depend on arrival order.
+template <int DT, int MB, int CB>
+__global__ __launch_bounds__(256) void mla_project_kernel(ProjectArgs a) {
+  constexpr int NW = 4;
+  constexpr int NT = MB * CB;             // 16 x 16 tiles per workgroup
+  constexpr int SLOT = CB * 2 * 1024;     // one chunk of the group's rows: CB x 2 blocks of 8 rows x 128 B
+  constexpr int WAVE_LDS = 2 * SLOT;      // two slots per wave
+  static_assert(NW * WAVE_LDS >= NW * NT * 1024, "tile sums fit the staging area");
+  __shared__ __attribute__((aligned(1024))) char smem[NW * WAVE_LDS];
+  __shared__ int s_last;
+  char LDS_AS* const lds = (char LDS_AS*)(void LDS_AS*)smem;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * 16 * CB;
+  const int C = a.k / 64, KS = gridDim.y, ks = blockIdx.y;
+  const int r0 = ks * C / KS, r1 = (ks + 1) * C / KS;
+  const int c0 = r0 + wave * (r1 - r0) / NW, c1 = r0 + (wave + 1) * (r1 - r0) / NW;
+  const int c = lane & 15, q = lane >> 4;
+  char LDS_AS* const mine = lds + wave * WAVE_LDS;
+  // copies: lane -> row 8 h + lane / 8 of column block cb, piece (lane % 8) ^ (lane / 8)
+  const int dr = lane >> 3, dp = (lane & 7) ^ dr;
+  const char* wsrc[CB][2];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      wsrc[cb][h] = reinterpret_cast<const char*>(a.w + (int64_t)(n0 + 16 * cb + 8 * h + dr) * a.w_s) + dp * 16;
+  auto issue = [&](int ch, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        lds_copy16<0>(wsrc[cb][h] + (int64_t)ch * 128, mine + slot * SLOT + (cb * 2 + h) * 1024);
+  };
+  // operand reads: row c of column block cb = block 2 cb + c / 8, row c % 8, piece (4 s + q) ^ (c % 8)
+  const int rd0 = (c >> 3) * 1024 + (c & 7) * 128;
+  const short* xp[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int row = min(mb * 16 + c, a.m - 1);  // rows past M repeat the last (never stored)
+    xp[mb] = a.x + (int64_t)row * a.x_s + q * 8;
+  }
+  f32x4 acc[MB][CB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) acc[mb][cb] = (f32x4)0.0f;
+  if (c0 < c1) issue(c0, 0);
+  for (int ch = c0; ch < c1; ++ch) {
+    const int slot = (ch - c0) & 1;
+    i16x8 xv[2][MB];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        xv[st][mb] = *reinterpret_cast<const i16x8*>(xp[mb] + (int64_t)ch * 64 + 32 * st);
+    if (ch + 1 < c1) {
+      issue(ch + 1, slot ^ 1);  // the next chunk in flight while this one is used
+      wait_vmcnt<2 * CB>();     // this chunk's copies and x loads have landed
+    } else {
+      wait_vmcnt<0>();
+    }
+    asm volatile("" ::: "memory");  // the operand reads below stay after the wait
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int off = rd0 + (((4 * st + q) ^ (c & 7)) << 4);
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const i16x8 wv = *reinterpret_cast<const i16x8 LDS_AS*>(mine + slot * SLOT + cb * 2048 + off);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[mb][cb] = mfma16<DT>(xv[st][mb], wv, acc[mb][cb]);
+      }
+    }
+  }
+  __syncthreads();  // every wave is done with its staging slots
+  f32x4 LDS_AS* red = (f32x4 LDS_AS*)lds;  // [NW][NT][64]
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) red[(wave * NT + mb * CB + cb) * 64 + lane] = acc[mb][cb];
+  __syncthreads();
+
+  // tile entry e = (mb * CB + cb) * 64 + lane holds rows mb * 16 + 4 * (lane / 16) .. +4 of column
+  // n0 + 16 * cb + lane % 16
+  auto sum_waves = [&](int e) __attribute__((always_inline)) {
+    f32x4 v = red[e];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += red[w * NT * 64 + e];
+    return v;
+  };
+  auto store_y = [&](int e, f32x4 v) __attribute__((always_inline)) {
+    const int t = e >> 6, l = e & 63, mb = t / CB, cb = t % CB;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = mb * 16 + 4 * (l >> 4) + r;
+      if (row < a.m) a.y[(int64_t)row * a.y_s + n0 + 16 * cb + (l & 15)] = Elt<DT>::from_float(v[r]);
+    }
+  };
+  if (KS == 1) {
+    for (int e = tid; e < NT * 64; e += 256) store_y(e, sum_waves(e));
+    return;
+  }
+  float* part = a.ws + ((int64_t)blockIdx.x * KS) * NT * 256;  // [KS][NT * 64] f32x4 of this column group
+  for (int e = tid; e < NT * 64; e += 256) store_through16(part + ((int64_t)ks * NT * 64 + e) * 4, sum_waves(e));
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores are complete
+  __syncthreads();
+  if (tid == 0) {
+    // release at device scope (the L2 written back, its completion awaited)
+    // before the arrival is counted, so the last workgroup, wherever it
+    // runs, reads every tile
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const int old = __hip_atomic_fetch_add(a.cnt + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    s_last = old == KS - 1;
+    if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(part, 0, KS * NT * 64 * 16, kBufferWord3);
+  for (int e = tid; e < NT * 64; e += 256) {
+    f32x4 v = (f32x4)0.0f;
+    for (int j = 0; j < KS; ++j)
+      v += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (j * NT * 64 + e) * 16, 0,
+                                                                           kSysCoherent));
+    store_y(e, v);
+  }
+  if (tid == 0) __hip_atomic_store(a.cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Launch shape of a projection: 64 columns per workgroup when N allows (x
+// read once per 4 weight tiles), and the contraction split over KS
+// workgroups so that about kProjectTargetWGs workgroups cover the chip,
+// with at least one 64-element chunk per wave.
+#ifndef TMLA_PROJECT_TARGET_WGS
+#define TMLA_PROJECT_TARGET_WGS 512
+#endif
+constexpr int kProjectTargetWGs = TMLA_PROJECT_TARGET_WGS;  // two resident per compute unit
+// The workspace starts with a fixed block of arrival counters (one per
+// column group, at most kProjectCounterBytes / 4 groups), the partial tiles
+// follow: whatever the shapes of the calls that share a workspace, no call's
+// tiles overlap any call's counters, and every call leaves its counters at
+// zero.
+constexpr size_t kProjectCounterBytes = 64 * 1024;
+struct ProjectPlan {
+  int cb, ks, groups;
+  size_t part_bytes, cnt_bytes;
+};
+ProjectPlan project_plan(int32_t m, int32_t n, int32_t k) {
+  ProjectPlan p;
+  p.cb = n % 64 == 0 ? 4 : 1;
+  p.groups = n / (16 * p.cb);
+  const int chunks = k / 64;
+  int ks = kProjectTargetWGs / p.groups;  // one round of resident workgroups
+  ks = min(ks, chunks / 4);  // at least one chunk per wave
+  p.ks = max(ks, 1);
+  const int mb = (m + 15) / 16;
+  p.part_bytes = p.ks > 1 ? (size_t)p.groups * p.ks * mb * p.cb * 64 * 16 : 0;
+  p.cnt_bytes = p.ks > 1 ? kProjectCounterBytes : 0;
+  return p;
+}
+
+template <int DT, int MB>
+hipError_t launch_project(const ProjectArgs& a, const ProjectPlan& p, hipStream_t s) {
+  const dim3 grid(p.groups, p.ks);
+  if (p.cb == 4)
+    hipLaunchKernelGGL((mla_project_kernel<DT, MB, 4>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((mla_project_kernel<DT, MB, 1>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_project_dt(const ProjectArgs& a, const ProjectPlan& p, hipStream_t s) {
+  switch ((a.m + 15) / 16) {
+    case 1: return launch_project<DT, 1>(a, p, s);
+    case 2: return launch_project<DT, 2>(a, p, s);
+    case 3: return launch_project<DT, 3>(a, p, s);
+    default: return launch_project<DT, 4>(a, p, s);
+  }
+}
+
 }  // namespace layer
 
 extern int fail(int code, const char* msg);
@@ -429,6 +723,81 @@ int tmla_mla_kv_append(const void* kv_proj, int64_t kv_proj_stride_b, const void
     hipLaunchKernelGGL(mla_kv_append_kernel<TMLA_FP16>, grid, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? TMLA_OK : hip_fail(e, "mla_kv_append_kernel launch");
+}
+
+int tmla_mla_rms_norm(const void* x, int64_t x_stride, const void* weight, float eps, int32_t rows, int32_t dim,
+                      int32_t dtype, void* y, int64_t y_stride, void* stream) {
+  if (rows < 0 || dim <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "rows must be >= 0 and dim > 0");
+  if (dtype != TMLA_BF16 && dtype != TMLA_FP16) return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16 or TMLA_FP16");
+  if (dim % 8 != 0) return fail(TMLA_ERR_UNSUPPORTED, "rms_norm is built for dim a multiple of 8");
+  if (rows == 0) return TMLA_OK;
+  if (!x || !y) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)weight) & 15)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "x, weight and y must be 16-byte aligned");
+  if ((x_stride | y_stride) & 7 || x_stride < dim || y_stride < dim)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "row strides must be multiples of 8 elements and >= dim");
+  RmsNormArgs a{};
+  a.x = static_cast<const short*>(x);
+  a.x_s = x_stride;
+  a.w = static_cast<const short*>(weight);
+  a.y = static_cast<short*>(y);
+  a.y_s = y_stride;
+  a.eps = eps;
+  a.rows = rows;
+  a.dim = dim;
+  dim3 grid((rows + 3) / 4);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TMLA_BF16)
+    hipLaunchKernelGGL(mla_rms_norm_kernel<TMLA_BF16>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(mla_rms_norm_kernel<TMLA_FP16>, grid, dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TMLA_OK : hip_fail(e, "mla_rms_norm_kernel launch");
+}
+
+size_t tmla_mla_project_workspace_bytes(int32_t m, int32_t n, int32_t k) {
+  if (m <= 0 || m > kProjectMaxRows || n <= 0 || n % 16 != 0 || k <= 0 || k % 64 != 0) return 0;
+  const ProjectPlan p = project_plan(m, n, k);
+  return p.part_bytes + p.cnt_bytes;
+}
+
+int tmla_mla_project(const void* x, int64_t x_stride, const void* w, int64_t w_stride, int32_t m, int32_t n,
+                     int32_t k, int32_t dtype, void* y, int64_t y_stride, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  if (m < 0 || n <= 0 || k <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "m must be >= 0, n and k > 0");
+  if (dtype != TMLA_BF16 && dtype != TMLA_FP16) return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16 or TMLA_FP16");
+  if (m > kProjectMaxRows || n % 16 != 0 || k % 64 != 0)
+    return fail(TMLA_ERR_UNSUPPORTED, "project is built for m <= 64, n a multiple of 16 and k a multiple of 64");
+  if (m == 0) return TMLA_OK;
+  if (!x || !w || !y) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (((uintptr_t)x | (uintptr_t)w) & 15 || (uintptr_t)y & 1)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "x and w must be 16-byte aligned, y 2-byte aligned");
+  if ((x_stride | w_stride) & 7 || x_stride < k || w_stride < k || y_stride < n)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "x and w row strides must be multiples of 8 elements and >= k, y's >= n");
+  const ProjectPlan p = project_plan(m, n, k);
+  if (p.ks > 1 && (size_t)p.groups * 4 > kProjectCounterBytes)
+    return fail(TMLA_ERR_UNSUPPORTED, "project splits the contraction of at most 16384 column groups");
+  const size_t need = p.part_bytes + p.cnt_bytes;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255)))
+    return fail(TMLA_ERR_WORKSPACE_TOO_SMALL,
+                "workspace is missing, smaller than tmla_mla_project_workspace_bytes() or not 256-byte aligned");
+  ProjectArgs a{};
+  a.x = static_cast<const short*>(x);
+  a.x_s = x_stride;
+  a.w = static_cast<const short*>(w);
+  a.w_s = w_stride;
+  a.y = static_cast<short*>(y);
+  a.y_s = y_stride;
+  a.m = m;
+  a.n = n;
+  a.k = k;
+  if (need > 0) {
+    a.cnt = static_cast<int32_t*>(workspace);
+    a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + kProjectCounterBytes);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = dtype == TMLA_BF16 ? launch_project_dt<TMLA_BF16>(a, p, s) : launch_project_dt<TMLA_FP16>(a, p, s);
+  return e == hipSuccess ? TMLA_OK : hip_fail(e, "mla_project_kernel launch");
 }
 
 }  // extern "C"

@@ -60,6 +60,10 @@ SIGNATURES = {
     "tmla_mla_kv_append": (ctypes.c_int, [
         _vp, _i64, _vp, _f32, _f32, _vp, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32,
         _vp]),
+    "tmla_mla_rms_norm": (ctypes.c_int, [_vp, _i64, _vp, _f32, _i32, _i32, _i32, _vp, _i64, _vp]),
+    "tmla_mla_project_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32]),
+    "tmla_mla_project": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _i64, _vp, ctypes.c_size_t,
+                                        _vp]),
 }
 
 STATUS = {0: "TMLA_OK", 1: "TMLA_ERR_INVALID_ARGUMENT", 2: "TMLA_ERR_UNSUPPORTED",

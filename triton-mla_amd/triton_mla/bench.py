@@ -119,6 +119,23 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
                          "eager_us": t_eager, "compile_us": t_compile})
 
 
+def capture_layer_step(model, x, cache, seqlens, bt, device):
+    """One MLA.forward step captured in a CUDA (HIP) graph on a side stream
+    of default priority, after two eager steps there that allocate the
+    step's cached buffers; returns the graph and its output tensor."""
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            model(x, cache, seqlens, bt)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out, _ = model(x, cache, seqlens, bt)
+    return graph, out
+
+
 def bench_layer(args, device, flush):
     """One MLA decode step at DeepSeek-V3 dims: HIP glue vs torch glue."""
     from .model import MLA, MLAConfig
@@ -133,8 +150,9 @@ def bench_layer(args, device, flush):
     model = model.to(device, DTYPES[args.dtype])
     weight_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
     print(f"# MLA layer step, DeepSeek-V3 dims, weights {weight_bytes / 1e6:.1f} MB, {args.dtype}")
-    print("| batch | context | hip glue us | torch glue us | mla_decode us | glue saved us | layer roofline us |")
-    print("|---|---|---|---|---|---|---|")
+    print("| batch | context | hip glue us | hip glue, graph us | torch glue us | mla_decode us | glue saved us "
+          "| layer roofline us |")
+    print("|---|---|---|---|---|---|---|---|")
     for batch in args.batch:
         for ctx in args.seqlen:
             page = args.page_size
@@ -150,12 +168,20 @@ def bench_layer(args, device, flush):
                 t_h = time_us(lambda: model(x, cache, seqlens, bt), reps=args.reps, flush=flush, device=device)
                 t_t = time_us(lambda: model.forward_torch_glue(x, cache, seqlens, bt), reps=args.reps, flush=flush,
                               device=device)
+                # the HIP-glue step captured in one graph (no host work between its kernels)
+                graph, out_g = capture_layer_step(model, x, cache, seqlens, bt, device)
+                graph.replay()
+                torch.cuda.synchronize(device)
+                assert torch.equal(out_g, out_h), "graph replay differs from the eager step"
+                t_g = time_us(graph.replay, reps=args.reps, flush=flush, device=device)
+                del graph, out_g
                 q = torch.randn(batch, cfg.num_heads, cfg.kv_cache_dim, generator=gen).to(device, cache.dtype)
                 call = DecodeLaunch(q, cache, seqlens + 1, bt, cfg.kv_lora_rank, cfg.qk_head_dim ** -0.5, None)
                 t_d = time_us(call.run, reps=args.reps, flush=flush, device=device)
             kv_bytes = batch * (ctx + 1) * cfg.kv_cache_dim * cache.element_size()
             roof = (weight_bytes + kv_bytes) / 8.0e12 * 1e6
-            print(f"| {batch} | {ctx} | {t_h['median']:.1f} | {t_t['median']:.1f} | {t_d['median']:.1f} | "
+            print(f"| {batch} | {ctx} | {t_h['median']:.1f} | {t_g['median']:.1f} | {t_t['median']:.1f} | "
+                  f"{t_d['median']:.1f} | "
                   f"{t_t['median'] - t_h['median']:.1f} | {roof:.1f} |", flush=True)
             del cache, bt, x, q, call
             torch.cuda.empty_cache()

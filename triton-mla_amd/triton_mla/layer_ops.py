@@ -1,11 +1,13 @@
 """HIP glue of the absorbed MLA decode step (the C ABI's tmla_mla_absorb_q,
-tmla_mla_kv_append and tmla_mla_absorb_out).
+tmla_mla_kv_append, tmla_mla_absorb_out and tmla_mla_project).
 
 These replace the torch steps of the reference layer around ``mla_decode``
 (src/triton_mla/model.py:74-124): the RoPE of q_pe and k_pe (model.py:44-50),
 the RMSNorm of the latent (model.py:34-41), the cache append
-(model.py:86-94) and the W_UK / W_UV einsums. Tensors stay on the GPU; there
-is no torch fallback.
+(model.py:86-94), the W_UK / W_UV einsums and, for a step's few rows, the
+dense projections (model.py:66-72). Tensors stay on the GPU; there is no
+torch fallback inside these functions (``project_fits`` tells the layer when
+a projection is one the kernel takes).
 """
 
 from __future__ import annotations
@@ -97,3 +99,94 @@ def kv_append(kv_proj, norm_weight, eps, rope_theta, positions, kv_cache, block_
             _native.DTYPE_CODE[kv_proj.dtype], kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1),
             num_blocks, page_size, *bt, _stream(dev)), "tmla_mla_kv_append")
     return kv_cache
+
+
+PROJECT_MAX_ROWS = 64  # rows of x tmla_mla_project takes
+# Where the kernel beats the library GEMM (measured at DeepSeek-V3 dims, 16
+# rows, one MI355X): wide weights (wq_b 24576 x 1536: 19.8 vs 30.0 us; wo
+# 7168 x 16384: 49.7 vs 49.2 us). Narrower ones leave it too few column
+# groups, and the contraction split it then needs costs more than the
+# library's time (wq_a 1536 x 7168: 17.9 vs 14.2 us; wkv_a 576 x 7168: 16.9
+# vs 13.7 us); more rows make its x reads as large as its weight reads
+# (wq_b at 64 rows: 33.4 vs 21.4 us).
+PROJECT_PAYS_ROWS = 16
+PROJECT_PAYS_COLUMNS = 4096
+
+
+def rms_norm(x, weight, eps):
+    """RMSNorm of the rows of a 2-D x (model.py:34-41): float32, the
+    normalised value times the weight rounded once (tmla_mla_rms_norm)."""
+    dev = _check_gpu(x)
+    assert x.dim() == 2 and x.stride(1) == 1
+    rows, dim = x.shape
+    if weight is not None:
+        weight = weight.to(device=dev, dtype=x.dtype).contiguous()
+    y = torch.empty(rows, dim, dtype=x.dtype, device=dev)
+    lib = _native.load()
+    with torch.cuda.device(dev):
+        _native.check(lib.tmla_mla_rms_norm(
+            x.data_ptr(), x.stride(0), None if weight is None else weight.data_ptr(), float(eps), rows, dim,
+            _native.DTYPE_CODE[x.dtype], y.data_ptr(), y.stride(0), _stream(dev)), "tmla_mla_rms_norm")
+    return y
+
+
+def project_pays(x, weight):
+    """Whether the layer should run y = x . weight^T with tmla_mla_project
+    rather than the library GEMM (the measurements above)."""
+    return (project_fits(x, weight) and x.shape[0] <= PROJECT_PAYS_ROWS
+            and weight.shape[0] >= PROJECT_PAYS_COLUMNS)
+
+
+def project_fits(x, weight):
+    """Whether tmla_mla_project takes y = x . weight^T: a 2-D 16-bit x of at
+    most 64 rows, weight [N, K] of the same dtype with N a multiple of 16,
+    K a multiple of 64, both with unit element stride and 16-byte aligned
+    rows."""
+    if x.dim() != 2 or weight.dim() != 2 or x.dtype not in _DTYPES or weight.dtype != x.dtype:
+        return False
+    if x.device.type != "cuda" or weight.device != x.device:
+        return False
+    m, k = x.shape
+    n = weight.shape[0]
+    if not (0 < m <= PROJECT_MAX_ROWS and weight.shape[1] == k and n % 16 == 0 and k % 64 == 0):
+        return False
+    if x.stride(1) != 1 or weight.stride(1) != 1 or x.stride(0) % 8 or weight.stride(0) % 8:
+        return False
+    return x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0
+
+
+_project_ws = {}  # device index -> zero-filled workspace of the split contractions (grown on demand)
+
+
+def _project_workspace(dev, nbytes):
+    """A zero-filled workspace of at least nbytes on dev, kept for later calls
+    (each call leaves its counters at zero). A larger buffer replaces a
+    smaller one; the old one stays valid for work already queued, since the
+    caching allocator reuses it only after the stream's earlier work."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    buf = _project_ws.get(idx)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _project_ws[idx] = buf
+    return buf
+
+
+def project(x, weight):
+    """y [M, N] = x [M, K] . weight [N, K]^T (nn.Linear without bias) for a
+    decode step's rows (model.py:66-82, 124): float32 accumulation in a fixed
+    order, rounded once to the dtype."""
+    dev = _check_gpu(x, weight)
+    if not project_fits(x, weight):
+        raise NotImplementedError("tmla_mla_project takes <= 64 rows, N % 16 == 0, K % 64 == 0, 16-byte aligned rows")
+    m, k = x.shape
+    n = weight.shape[0]
+    y = torch.empty(m, n, dtype=x.dtype, device=dev)
+    lib = _native.load()
+    need = lib.tmla_mla_project_workspace_bytes(m, n, k)
+    ws = _project_workspace(dev, need) if need else None
+    with torch.cuda.device(dev):
+        _native.check(lib.tmla_mla_project(
+            x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), m, n, k, _native.DTYPE_CODE[x.dtype],
+            y.data_ptr(), y.stride(0), None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+            _stream(dev)), "tmla_mla_project")
+    return y

@@ -9,7 +9,9 @@ and ``forward_naive`` (decompressed per-head K/V, model.py:126-144). In
 ``forward`` the attention is the HIP ``mla_decode`` and the glue around it
 runs as HIP kernels too (triton_mla.layer_ops): the cache append (RMSNorm of
 the latent, RoPE of the key, paged write), the W_UK absorption with the q_pe
-RoPE, and the W_UV product; the dense projections stay library GEMMs.
+RoPE, the W_UV product, the RMSNorm of the query latent, and the wide dense
+projections (wq_b, wo) of a step of up to 16 rows; wq_a and wkv_a run as one
+library GEMM over both weights.
 ``forward_naive`` keeps the reference's torch steps: it is the layer's
 oracle.
 """
@@ -20,6 +22,7 @@ from dataclasses import dataclass
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import layer_ops
 from .kernel import mla_decode
@@ -148,8 +151,11 @@ class MLA(nn.Module):
             # the HIP glue runs in the layer's 16-bit dtype; other dtype mixes
             # take the reference's torch glue, which casts (model.py:108-124)
             return self.forward_torch_glue(x, kv_cache, cache_seqlens, block_table, num_splits)
-        q_proj = self.wq_b(self.q_norm(self.wq_a(x)))  # [B, H * (nope + rope)]
-        kv_proj = self.wkv_a(x)  # [B, rank + rope]
+        # wq_a and wkv_a read the same rows: one GEMM over both weights
+        down = F.linear(x, self._down_weight())  # [B, q_lora_rank + rank + rope]
+        q_lat, kv_proj = down[:, :cfg.q_lora_rank], down[:, cfg.q_lora_rank:]
+        q_lat = layer_ops.rms_norm(q_lat, self.q_norm.weight, self.q_norm.eps)
+        q_proj = self._linear(self.wq_b, q_lat)  # [B, H * (nope + rope)]
         # RMSNorm(c_kv), RoPE(k_pe) and the paged append (model.py:80-94)
         layer_ops.kv_append(kv_proj, self.kv_norm.weight, self.kv_norm.eps, cfg.rope_theta, cache_seqlens,
                             kv_cache, block_table, cfg.kv_lora_rank, cfg.qk_rope_head_dim)
@@ -162,7 +168,27 @@ class MLA(nn.Module):
         # o . W_UV^T per head (model.py:120-124), then wo
         o = layer_ops.absorb_out(o, self.wkv_b.weight, cfg.num_heads, cfg.qk_nope_head_dim, cfg.kv_lora_rank,
                                  cfg.v_head_dim)
-        return self.wo(o), seqlens
+        return self._linear(self.wo, o), seqlens
+
+    @staticmethod
+    def _linear(layer, x):
+        """A projection of the step's rows: the HIP kernel where it beats the
+        library GEMM (few rows, a wide weight), the library GEMM otherwise."""
+        if layer.bias is None and layer_ops.project_pays(x, layer.weight):
+            return layer_ops.project(x, layer.weight)
+        return layer(x)
+
+    def _down_weight(self):
+        """[wq_a; wkv_a] as one [q_lora_rank + rank + rope, hidden] weight,
+        rebuilt when either parameter is replaced or changed in place."""
+        wa, wk = self.wq_a.weight, self.wkv_a.weight
+        key = (wa.data_ptr(), wa._version, wk.data_ptr(), wk._version, wa.dtype, wa.device)
+        cached = getattr(self, "_down_cache", None)
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                cached = (key, torch.cat([wa.detach(), wk.detach()], dim=0))
+            self._down_cache = cached
+        return cached[1]
 
     def forward_torch_glue(self, x, kv_cache, cache_seqlens, block_table=None, num_splits=None):
         """The absorbed step with the reference's torch glue around the HIP
