@@ -54,12 +54,12 @@ int tmla_version(void);
  * Bytes of device workspace tmla_mla_decode / _partial / _combine / _fused
  * need: partial outputs (input dtype [slots, H, head_dim_v]) and their
  * base-2 log-sum-exps (float32 [slots, H]) from the start of the buffer, and
- * the int32 counters of the single launch's merge in a block at the END of
- * the buffer (its size rounded down to 256 bytes);
+ * a block of fixed size (256 KiB) at the END of the buffer (its size rounded
+ * down to 256 bytes) for the int32 counters of the single launch's merge;
  * slots = batch * num_splits (uniform) or num_workers + batch (balanced).
  * The two-kernel entry points need no initialisation. A workspace may be
- * reused by any later call whose tmla_workspace_bytes is no larger, one
- * call at a time.
+ * reused by any later call whose tmla_workspace_bytes is no larger, of any
+ * shape, one call at a time.
  */
 size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v,
                             int32_t num_splits, int32_t num_workers);
@@ -68,10 +68,13 @@ size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v
  * Bytes at the end of the workspace that must be zero before its first use
  * by tmla_mla_decode_fused (or tmla_mla_decode_causal with single_launch):
  * zero the last min(tmla_workspace_zero_bytes(...), workspace_bytes) bytes
- * once, with the arguments of the largest call the buffer will serve. Every
- * single launch leaves its counters at zero again, and the partials of no
- * call reach that suffix, so later calls of any size up to it need nothing.
- * No counterpart in the reference (its two launches need no counters).
+ * once (the counter block and the rounding slack; the same for every call).
+ * Every single launch leaves its counters at zero again, and the partials of
+ * no call reach that suffix, so later calls of any shape whose
+ * tmla_workspace_bytes fits the buffer need nothing. A call whose counters
+ * would not fit the block ((2 * batch + slots) * head blocks > 65536) runs as
+ * two kernels. No counterpart in the reference (its two launches need no
+ * counters).
  */
 size_t tmla_workspace_zero_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v,
                                  int32_t num_splits, int32_t num_workers);

@@ -44,19 +44,23 @@ def _al(x):
     return (x + 255) // 256 * 256
 
 
-def _counter_bytes(batch, slots, heads):
+COUNTER_BLOCK = 256 * 1024  # the single launch's counter block, the same for every call
+
+
+def _counter_ints(batch, slots, heads):
     # the single launch's int32 counters: 2 per (sequence, head block) and 1
     # per (slot, head block), head blocks of up to 128 heads
     gy = -(-heads // (32 if heads <= 32 else 64 if heads <= 64 else 128))
-    return _al((2 * batch + slots) * gy * 4)
+    return (2 * batch + slots) * gy
 
 
 def test_workspace_arithmetic(lib):
     # uniform: batch * splits slots; balanced: workers + batch slots (16-bit
-    # partial + float32 lse, each region 256-byte aligned), then the counter
-    # block (256-byte aligned) that the kernels place at the buffer's end
+    # partial + float32 lse, each region 256-byte aligned), then the fixed
+    # counter block that the kernels place at the buffer's end
     def expect(batch, slots, heads, dv=512):
-        return _al(slots * heads * dv * 2) + _al(slots * heads * 4) + _counter_bytes(batch, slots, heads)
+        assert _counter_ints(batch, slots, heads) * 4 <= COUNTER_BLOCK
+        return _al(slots * heads * dv * 2) + _al(slots * heads * 4) + COUNTER_BLOCK
 
     assert lib.tmla_workspace_bytes(32, 128, 512, 8, 0) == expect(32, 256, 128)
     assert lib.tmla_workspace_bytes(32, 128, 512, 0, 256) == expect(32, 288, 128)
@@ -67,11 +71,11 @@ def test_workspace_arithmetic(lib):
 
 def test_workspace_zero_suffix(lib):
     # the suffix to clear before the first single launch: the counter block
-    # plus the slack of rounding the buffer size down to 256 bytes
+    # plus the slack of rounding the buffer size down to 256 bytes, the same
+    # for every call (so calls of any shape can share a buffer)
     for batch, heads, splits, workers in [(32, 128, 0, 256), (8, 128, 0, 256), (3, 20, 1, 0), (4, 256, 2, 0)]:
-        slots = batch * splits if splits else workers + batch
         z = lib.tmla_workspace_zero_bytes(batch, heads, 512, splits, workers)
-        assert z == _counter_bytes(batch, slots, heads) + 255
+        assert z == COUNTER_BLOCK + 255
         assert z < lib.tmla_workspace_bytes(batch, heads, 512, splits, workers)
     # a smaller call's counters fit inside a larger call's suffix
     assert lib.tmla_workspace_zero_bytes(8, 128, 512, 0, 256) <= lib.tmla_workspace_zero_bytes(32, 128, 512, 0, 256)

@@ -160,6 +160,36 @@ def test_workspace_reuse_across_sizes(gpu):
         assert_same((c.out.clone(), c.lse.clone()), refs[name], f"{name} on the shared workspace")
 
 
+def test_workspace_reuse_across_shapes(gpu):
+    """Calls of other shapes on one workspace: a 16-head call with more
+    sequences has a larger counter set but a smaller workspace than the
+    128-head headline call that sized the buffer; its counters stay clear of
+    the headline call's partials (the counter block is the same fixed size for
+    every call), so both keep the two-kernel bits in any order."""
+    from triton_mla import _native, workloads
+
+    lib = _native.load()
+    big = launch(workloads.b32_h128_8k(), gpu)
+    wide = launch(workloads.ragged_b64_h16(), gpu)
+    calls = {"big": big, "wide": wide}
+    for name, c in calls.items():
+        assert c.fused, f"{name} must take the single-launch path"
+    assert wide.ws_bytes <= big.ws_bytes
+    refs = {name: two_stage(c) for name, c in calls.items()}
+    ws = torch.full((big.ws_bytes,), 0x5A, dtype=torch.uint8, device=gpu)
+    z = min(lib.tmla_workspace_zero_bytes(big.batch, big.num_heads, 512, big.splits, big.workers), big.ws_bytes)
+    assert z == lib.tmla_workspace_zero_bytes(wide.batch, wide.num_heads, 512, wide.splits, wide.workers)
+    ws[big.ws_bytes - z:].zero_()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    for name in ["big", "wide", "big", "wide"]:
+        c = calls[name]
+        c.out.fill_(1.0)
+        c.lse.fill_(1.0)
+        fused_on(lib, c, ws, stream)
+        torch.cuda.synchronize()
+        assert_same((c.out.clone(), c.lse.clone()), refs[name], f"{name} on the shared workspace")
+
+
 def test_fuse_decision_matches_launch(gpu):
     """DecodeLaunch.fused comes from the library's own plan: a call it
     reports as single-launch needs no combine kernel (stage 2 after it would

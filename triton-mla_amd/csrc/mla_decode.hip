@@ -1749,26 +1749,34 @@ int head_blocks(int32_t heads) {
 // Workspace of a call: partial rows [slots, H, dv] (input dtype) at offset 0,
 // their base-2 lse [slots, H] (float) after them, and the fused merge's int32
 // counters m_count and m_done [batch, head blocks] and flags m_flag [slots,
-// head blocks] in a block anchored at the END of the caller's buffer (its size
-// rounded down to 256 bytes). Anchored there, the counter block of every call
-// no larger than the one the buffer was sized for lies in the same suffix,
-// which no call's partials reach: the suffix is zero-filled once, and every
-// single launch leaves its counters at zero again.
+// head blocks] at the start of a block of fixed size (kFusedCounterBytes)
+// anchored at the END of the caller's buffer (its size rounded down to 256
+// bytes). Every call reserves the whole block, so no call's partials reach
+// it, whatever the shapes of the calls that share the buffer: the block is
+// zero-filled once, and every single launch leaves its counters at zero
+// again. A call whose counters exceed the block runs as two kernels.
 struct WsLayout {
   size_t o, l, part_end;  // byte offsets: partial rows, lse, end of both
   size_t cnt_bytes;       // counter block (a multiple of 256)
   size_t total;           // part_end + cnt_bytes: the bytes the call needs
 };
 
+constexpr size_t kFusedCounterBytes = 256 * 1024;
+
+// Bytes of the fused merge's counters and flags of a call.
+int64_t fused_counter_bytes(int32_t batch, int32_t heads, int32_t splits, int32_t workers) {
+  const int64_t slots = splits > 0 ? (int64_t)batch * splits : (int64_t)workers + batch;
+  return (2 * (int64_t)batch + slots) * head_blocks(heads) * 4;
+}
+
 WsLayout ws_layout(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
   auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
   const int64_t slots = splits > 0 ? (int64_t)batch * splits : (int64_t)workers + batch;
-  const int64_t gy = head_blocks(heads);
   WsLayout w;
   w.o = 0;
   w.l = al((size_t)slots * heads * dv * 2);
   w.part_end = w.l + al((size_t)slots * heads * sizeof(float));
-  w.cnt_bytes = al((size_t)(2 * (int64_t)batch + slots) * gy * 4);
+  w.cnt_bytes = kFusedCounterBytes;
   w.total = w.part_end + w.cnt_bytes;
   return w;
 }
@@ -1832,7 +1840,8 @@ LaunchPlan plan_launch(int32_t batch, int32_t num_heads, int32_t num_splits, int
   p.grid = dim3(grid_x, (num_heads + heads_per_wg - 1) / heads_per_wg);
   // The fused merge: one workgroup per compute unit at most (the kernel's LDS
   // use admits one), so that siblings normally run side by side.
-  p.fused = mode == 1 && (int64_t)p.grid.x * p.grid.y <= cus && mid_o_bytes < (size_t)INT32_MAX;
+  p.fused = mode == 1 && (int64_t)p.grid.x * p.grid.y <= cus && mid_o_bytes < (size_t)INT32_MAX &&
+            fused_counter_bytes(batch, num_heads, num_splits, num_workers) <= (int64_t)kFusedCounterBytes;
   return p;
 }
 
