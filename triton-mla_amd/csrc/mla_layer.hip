@@ -524,13 +524,10 @@ __global__ __launch_bounds__(256) void mla_project_kernel(ProjectArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores are complete
   __syncthreads();
   if (tid == 0) {
-    // release at device scope (the L2 written back, its completion awaited)
-    // before the arrival is counted, so the last workgroup, wherever it
-    // runs, reads every tile
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    // the tiles were written through to memory and their stores completed
+    // before this arrival; the last workgroup reads them past its caches
     const int old = __hip_atomic_fetch_add(a.cnt + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     s_last = old == KS - 1;
-    if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (!s_last) return;
