@@ -187,6 +187,33 @@ def bench_layer(args, device, flush):
             torch.cuda.empty_cache()
 
 
+def bench_projections(args, device, flush):
+    """The MLA layer's dense projections at DeepSeek-V3 dims for --batch rows:
+    tmla_mla_project against the library GEMM (torch.nn.functional.linear)."""
+    import torch.nn.functional as F
+
+    from . import layer_ops
+
+    cfg_shapes = {"wq_a": (1536, 7168), "wq_b": (128 * 192, 1536), "wkv_a": (576, 7168), "wo": (7168, 128 * 128)}
+    gen = torch.Generator(device=device).manual_seed(0)
+    dtype = DTYPES[args.dtype]
+    print(f"# MLA layer projections, DeepSeek-V3 dims, {args.dtype}")
+    print("| rows | projection | N x K | weight MB | library us | tmla_mla_project us | project TB/s |")
+    print("|---|---|---|---|---|---|---|")
+    for m in args.batch:
+        for name, (n, k) in cfg_shapes.items():
+            x = torch.randn(m, k, device=device, generator=gen).to(dtype)
+            w = (0.02 * torch.randn(n, k, device=device, generator=gen)).to(dtype)
+            if not layer_ops.project_fits(x, w):
+                continue
+            lib_t = time_us(lambda: F.linear(x, w), reps=args.reps, flush=flush, device=device)["median"]
+            hip_t = time_us(lambda: layer_ops.project(x, w), reps=args.reps, flush=flush, device=device)["median"]
+            mb = n * k * w.element_size() / 1e6
+            print(f"| {m} | {name} | {n} x {k} | {mb:.1f} | {lib_t:.2f} | {hip_t:.2f} | {mb / hip_t:.2f} |",
+                  flush=True)
+            del x, w
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--batch", type=int, nargs="+", default=[1, 8, 32, 64, 128])
@@ -207,11 +234,16 @@ def main(argv=None):
                              "PyTorch baselines decode the dequantised values")
     parser.add_argument("--layer", action="store_true",
                         help="time the MLA layer step at DeepSeek-V3 dims (HIP glue vs torch glue)")
+    parser.add_argument("--projections", action="store_true",
+                        help="time the layer's dense projections for --batch rows (HIP kernel vs library GEMM)")
     args = parser.parse_args(argv)
 
     device = torch.device("cuda")
     dtype = DTYPES[args.dtype]
     flush = Flusher(device)
+    if args.projections:
+        bench_projections(args, device, flush)
+        return
     if args.layer:
         bench_layer(args, device, flush)
         return
