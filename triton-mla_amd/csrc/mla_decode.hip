@@ -1763,10 +1763,11 @@ struct WsLayout {
 
 constexpr size_t kFusedCounterBytes = 256 * 1024;
 
-// Bytes of the fused merge's counters and flags of a call.
-int64_t fused_counter_bytes(int32_t batch, int32_t heads, int32_t splits, int32_t workers) {
+// Bytes of the fused merge's counters and flags of a call whose grid has gy
+// workgroups along the heads.
+int64_t fused_counter_bytes(int32_t batch, int64_t gy, int32_t splits, int32_t workers) {
   const int64_t slots = splits > 0 ? (int64_t)batch * splits : (int64_t)workers + batch;
-  return (2 * (int64_t)batch + slots) * head_blocks(heads) * 4;
+  return (2 * (int64_t)batch + slots) * gy * 4;
 }
 
 WsLayout ws_layout(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
@@ -1830,18 +1831,18 @@ LaunchPlan plan_launch(int32_t batch, int32_t num_heads, int32_t num_splits, int
   p.nhb = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
   // When the busy workgroups would leave compute units idle, fewer heads per
   // workgroup (more, shorter workgroups: less Q to load, less MFMA work per
-  // sub-tile, smaller partial rows) use them. The single-launch merge keeps
-  // the head blocks its counters are laid out for.
+  // sub-tile, smaller partial rows) use them. (Halving keeps grid.x * grid.y
+  // within the compute units, so it never takes a call off the single launch.)
   const int grid_x = worker_grid(batch, num_splits, num_workers, capacity_tokens);
-  if (mode != 1) {
-    while (p.nhb > 1 && (int64_t)grid_x * ((num_heads + 16 * p.nhb - 1) / (16 * p.nhb)) <= cus) p.nhb /= 2;
-  }
+  while (p.nhb > 1 && (int64_t)grid_x * ((num_heads + 16 * p.nhb - 1) / (16 * p.nhb)) <= cus) p.nhb /= 2;
   const int heads_per_wg = 32 * p.nhb;
   p.grid = dim3(grid_x, (num_heads + heads_per_wg - 1) / heads_per_wg);
   // The fused merge: one workgroup per compute unit at most (the kernel's LDS
-  // use admits one), so that siblings normally run side by side.
+  // use admits one), so that siblings normally run side by side; its
+  // counters (per sequence and per slot, for each workgroup along the heads)
+  // fit the workspace's counter block.
   p.fused = mode == 1 && (int64_t)p.grid.x * p.grid.y <= cus && mid_o_bytes < (size_t)INT32_MAX &&
-            fused_counter_bytes(batch, num_heads, num_splits, num_workers) <= (int64_t)kFusedCounterBytes;
+            fused_counter_bytes(batch, p.grid.y, num_splits, num_workers) <= (int64_t)kFusedCounterBytes;
   return p;
 }
 
@@ -2007,14 +2008,6 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   const WsLayout wl = ws_layout(batch, num_heads, 512, num_splits, num_workers);
   a.mid_o = reinterpret_cast<short*>(ws + wl.o);
   a.mid_lse = reinterpret_cast<float*>(ws + wl.l);
-  // counters at the end of the caller's buffer (check_common: it holds
-  // wl.total bytes, a multiple of 256, so the block starts at or after
-  // wl.part_end)
-  const int64_t gy_ws = head_blocks(num_heads);
-  char* cnt = ws + ((workspace_bytes_ & ~(size_t)255) - wl.cnt_bytes);
-  a.m_count = reinterpret_cast<int32_t*>(cnt);
-  a.m_done = a.m_count + (int64_t)batch * gy_ws;
-  a.m_flag = a.m_done + (int64_t)batch * gy_ws;
   a.spin_limit = spin_limit >= 0 ? spin_limit : kDefaultSpinLimit;
 
   const int64_t cap_tokens = paged ? (int64_t)bt_cols * page_size : num_blocks;
@@ -2056,6 +2049,14 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   const dim3 grid = plan.grid;
   a.mid_o_bytes = (int32_t)(mid_o_bytes < (size_t)INT32_MAX ? mid_o_bytes : 0);
   a.fused = plan.fused ? 1 : 0;
+  // the single launch's counters and flags [batch | batch | slots][grid.y] at
+  // the start of the counter block at the end of the caller's buffer
+  // (check_common: it holds wl.total bytes, a multiple of 256, so the block
+  // starts at or after wl.part_end)
+  char* cnt = ws + ((workspace_bytes_ & ~(size_t)255) - wl.cnt_bytes);
+  a.m_count = reinterpret_cast<int32_t*>(cnt);
+  a.m_done = a.m_count + (int64_t)batch * grid.y;
+  a.m_flag = a.m_done + (int64_t)batch * grid.y;
   hipError_t e = dtype == TMLA_BF16 ? launch_partial_dt<TMLA_BF16>(a, grid, nhb, s, paged, uni)
                                     : launch_partial_dt<TMLA_FP16>(a, grid, nhb, s, paged, uni);
   if (e != hipSuccess) return hip_fail(e, "mla_partial_kernel launch");
