@@ -99,6 +99,20 @@ __device__ __forceinline__ int piece_swizzle(int r, int rg) {
   return (((r >> 1) & 1) << 2) | ((r >> 2) & 1) | ((rg & 1) << 1);
 }
 
+// Reductions over the four 16-lane rows of a wave without the LDS pipe.
+// v_permlane16_swap_b32 a, b swaps the odd 16-lane rows of a with the even
+// rows of b, v_permlane32_swap_b32 the upper 32 lanes of a with the lower 32
+// of b: with x in both, a and b then hold x of the two rows (halves) of each
+// pair, so combining them reduces over the pair. As asm, with both registers
+// read and written (the builtins' second result is not usable here); the
+// s_nop is the wait state a VALU result needs before the swap reads it.
+__device__ __forceinline__ void swap_rows16(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap_rows32(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I = 0..N-1, so
 // LDS offsets can be instruction immediates.
 template <class F, int... Is>

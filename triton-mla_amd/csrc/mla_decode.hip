@@ -1640,6 +1640,706 @@ void mla_partial_kernel(PartialArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Stage 1 at 128 heads per workgroup: the head-owner loop
+// ---------------------------------------------------------------------------
+//
+// Wave w owns heads 32w..32w+31 of the workgroup for the whole computation:
+// S^T = K . Q^T (36 MFMAs per 32-token sub-tile), the online softmax of its
+// heads, and O^T += V^T . P^T over all 512 value dims (16 accumulator blocks
+// of 32 dims x 32 heads in AGPRs, 32 MFMAs per sub-tile). P^T is the score
+// tile itself, rounded in place: the 32x32 accumulator holds, in lane l,
+// head l%32 and tokens 8(r/4) + 4(l/32) + r%4 in register r, so registers
+// 0-7 are the B operand of the value product's k-step over tokens 0-15 and
+// registers 8-15 that of tokens 16-31, with k taken in that token order; the
+// V^T operand reads (ds_read_b64_tr_b16, addressing as in
+// mla_partial_kernel) deliver the same order. No wave reads another wave's
+// probabilities, so the workgroup barrier of an iteration only hands ring
+// entries back to the copies.
+//
+// Iteration i of a segment (sub-tiles i and i+1 in the ring, i+2 and i+3 in
+// flight): one run of steps that first issues the S^T MFMAs of sub-tile i+1,
+// one K read each, beside the softmax of sub-tile i (whose scores the
+// previous iteration computed) and the copies of sub-tile i+3, then the 32
+// value MFMAs of sub-tile i, two V^T reads each, with the probabilities
+// straight from registers. The softmax VALU work thus runs under MFMAs whose
+// operands do not depend on it. Two score tiles alternate (one is turned into
+// probabilities while the other accumulates), and the loop body is written
+// out for both. When the reference max of a head moves (the lazy rescale,
+// rare), O^T is rescaled before the value MFMAs of the sub-tile.
+//
+// LDS: V ring (dims 0..511, 4 entries) and rope ring (dims 512..575, 3
+// entries) in mla_partial_kernel's swizzled block layout, and the rope rows of
+// Q (read as the Q^T operand of the rope k-chunks, whose registers the loop
+// cannot spare); 156 KiB.
+// 1: 128-head workgroups run the head-owner loop (0: mla_partial_kernel)
+#ifndef TMLA_OWN_LOOP
+#define TMLA_OWN_LOOP 1
+#endif
+#ifndef TMLA_OWN_READ_AHEAD
+#define TMLA_OWN_READ_AHEAD 3
+#endif
+// softmax schedule inside the step run of an iteration: first exponential at
+// this step, then one every TMLA_OWN_EXP_STRIDE steps
+#ifndef TMLA_OWN_EXP_START
+#define TMLA_OWN_EXP_START 4
+#endif
+#ifndef TMLA_OWN_EXP_STRIDE
+#define TMLA_OWN_EXP_STRIDE 2
+#endif
+// steps of an iteration's run that issue the copies of sub-tile i+3: from
+// step TMLA_OWN_COPY_FIRST, spread over TMLA_OWN_COPY_SPAN steps
+#ifndef TMLA_OWN_COPY_FIRST
+#define TMLA_OWN_COPY_FIRST 1
+#endif
+#ifndef TMLA_OWN_COPY_SPAN
+#define TMLA_OWN_COPY_SPAN 32
+#endif
+// operand registers beyond the read-ahead (an MFMA queued behind the one
+// before it may read its operands after the next fetch was issued)
+#ifndef TMLA_OWN_EXTRA_BUF
+#define TMLA_OWN_EXTRA_BUF 0
+#endif
+// S^T accumulated in this many chains (1 or 2) over alternate k-chunks
+#ifndef TMLA_OWN_S_CHAINS
+#define TMLA_OWN_S_CHAINS 2
+#endif
+// the next sub-tile's max this many value steps after its last S^T MFMA
+#ifndef TMLA_OWN_MAX_LAG
+#define TMLA_OWN_MAX_LAG 8
+#endif
+
+// S^T MFMAs of the head-owner loop: volatile asm, so they keep their places
+// among the operand reads and waits and keep their accumulators in VGPRs
+// (the value accumulators own every AGPR). The VALU reads of their results
+// are placed a fixed number of steps later, past the result latency.
+template <int DT>
+__device__ __forceinline__ f32x16 own_mfma_first(const i16x8& a, const i16x8& b) {
+  f32x16 d;
+  if constexpr (DT == TMLA_BF16)
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  return d;
+}
+template <int DT>
+__device__ __forceinline__ void own_mfma_acc(f32x16& d, const i16x8& a, const i16x8& b) {
+  if constexpr (DT == TMLA_BF16)
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+}
+
+// LDS reads issued by step t of a run of NS S^T steps and NV value steps
+// (the rope k-chunks 32..35 read Q^T from LDS beside K).
+template <int NS, int NV>
+constexpr int own_step_reads(int t) {
+  return t < NS ? (t < 32 ? 1 : 2) : (t < NS + NV ? 2 : 0);
+}
+
+template <int DT, bool PAGED, bool PAGE_UNIFORM>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void mla_partial_own_kernel(PartialArgs a) {
+  constexpr int DV = 512, DQK = 576;
+  constexpr int NCB = DQK / 64;   // 128-byte column blocks per row
+  constexpr int NVB = DV / 64;    // ... of which hold V dims
+  constexpr int NRB = NCB - NVB;  // ... and rope dims
+  constexpr int NKC = DQK / 16;   // k-chunks of QK^T
+  constexpr int NDB = DV / 32;    // 32-dim blocks of PV (all of them per wave)
+  constexpr int VSLOT = 4 * NVB * 1024;
+  constexpr int RSLOT = 4 * NRB * 1024;
+  constexpr int RING = 4;         // entries of both rings
+  constexpr int RRING = RING - 1;  // rope entries: dead once S of their sub-tile is done
+  constexpr int OFF_R = RING * VSLOT;
+  constexpr int OFF_Q = OFF_R + RRING * RSLOT;  // Q rope rows of the workgroup (read as Q^T)
+  constexpr int SMEM = OFF_Q + 4 * RSLOT;
+  constexpr int NKQ = DV / 16;    // k-chunks whose Q^T operand stays in VGPRs
+  constexpr int LOADS = NCB;      // DMA instructions per wave per sub-tile (row-group `wave`)
+  constexpr int OPITCH = DV * 2 + 16;
+  constexpr int PD = TMLA_OWN_READ_AHEAD;
+  // operand registers of a step are refilled NOB steps after their fetch:
+  // at least two steps after the MFMA that read them was issued
+  constexpr int NOB = PD + 1 + TMLA_OWN_EXTRA_BUF;
+  constexpr int E0 = TMLA_OWN_EXP_START, ES = TMLA_OWN_EXP_STRIDE;
+  constexpr int MX = NKC + TMLA_OWN_MAX_LAG;  // step of the next sub-tile's max
+  constexpr int SCH = TMLA_OWN_S_CHAINS;      // accumulation chains of S^T
+  // the copies of sub-tile i+3: at steps CP0 + k * CPS / LOADS, k < LOADS
+  constexpr int CP0 = TMLA_OWN_COPY_FIRST, CPS = TMLA_OWN_COPY_SPAN;
+  static_assert(NRB == 1 && NKC == 36 && NDB == 16 && NKQ == 32, "512 latent + 64 rope dims");
+  static_assert(128 * OPITCH <= SMEM, "output staging fits the rings");
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  static_assert(PD >= 1 && PD <= 4, "read-ahead");
+  static_assert(SCH == 1 || SCH == 2, "S^T chains");
+  static_assert(CP0 >= 1 && CP0 + (LOADS - 1) * CPS / LOADS < NKC + 2 * NDB, "copy schedule");
+  // the probabilities of tokens 0-15 (exponentials 0-7) are packed before the
+  // first value step, those of tokens 16-31 before the value steps of k-step 1
+  static_assert(E0 >= 1 && E0 + 7 * ES + 1 < NKC && E0 + 15 * ES + 1 < NKC + NDB, "softmax schedule");
+  static_assert(MX >= NKC + 6 && MX + 5 <= NKC + 2 * NDB, "max after the S^T results are ready");
+
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+  char LDS_AS* const lds = (char LDS_AS*)(void LDS_AS*)smem;
+  __shared__ int s_pend[2][5];
+  __shared__ int s_msg[4];
+
+  phase_stamp(0);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwg = gridDim.x;
+  const int worker = worker_index(a);
+  const int head_base = blockIdx.y * 128 + wave * kHeadsPerWave;
+  const int lag_wave = __builtin_amdgcn_readfirstlane(causal_lag(a, head_base));
+  const int pre_len = __builtin_amdgcn_readfirstlane((a.fused && worker < a.batch) ? a.seqlens[worker] : 1);
+  if (a.fused && tid == 0) s_pend[0][0] = s_pend[1][0] = -1;
+
+  // Q rows of sequence bq for this wave's heads into V ring entry `wave` and
+  // rope entry `wave`, in the KV copies' swizzled layout (heads past
+  // num_heads copy head 0's row).
+  auto stage_q = [&](int bq) __attribute__((always_inline)) {
+    const int ln = lane_id_fresh();
+    const int r = ln >> 3;
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const int hq = head_base + 8 * rg + r;
+      const char* src = a.q + ((int64_t)bq * a.q_sb + (int64_t)(hq < a.num_heads ? hq : 0) * a.q_sh) * 2 +
+                        ((ln & 7) ^ piece_swizzle(r, rg)) * 16;
+      static_for<NCB>([&](auto CB) __attribute__((always_inline)) {
+        constexpr int cb = decltype(CB)::value;
+        char LDS_AS* dst = cb < NVB ? lds + wave * VSLOT + (rg * NVB + cb) * 1024
+                                    : lds + OFF_Q + wave * RSLOT + (rg * NRB + cb - NVB) * 1024;
+        lds_copy16<cb * 128>(src, dst);
+      });
+    }
+  };
+
+  // ---- work range -------------------------------------------------------
+  WorkRange wr;
+  if (!work_range(a, worker, wr)) {
+    if (!a.fused) return;
+  }
+  const int b_first = wr.b_first, tile_lo = wr.tile_lo, tile_hi = wr.tile_hi;
+  const int off_first = wr.off_first, n_first = wr.n_first;
+  if (a.fused) {
+    // empty sequences worker, worker + nwg, ...: out = 0, lse = -inf
+    const int lane = lane_id_fresh();
+    const int hb0 = blockIdx.y * 128;
+    const int nh = min(128, a.num_heads - hb0);
+    const MergeView mv{a.mid_o, a.mid_lse, a.num_heads, a.out, a.out_sb, a.out_sh, a.lse};
+    for (int bb = worker; bb < a.batch; bb += nwg) {
+      const int len = bb == worker ? pre_len : a.seqlens[bb];
+      if (tiles_of(len) == 0)
+        for (int h = hb0 + wave; h < hb0 + nh; h += 4) merge_zero(mv, bb, h, lane);
+    }
+  }
+  if (tile_lo >= tile_hi) return;
+  phase_stamp(1);
+
+  int b = b_first;
+  int t_start = tile_lo;
+  int remaining = tile_hi - tile_lo;
+  int seg_global_off = off_first;
+
+  while (remaining > 0) {
+    const int n_b = b == b_first ? n_first : a.seqlens[b];
+    const int nt_b = tiles_of(n_b);
+    if (nt_b == 0) {
+      ++b;
+      continue;
+    }
+    const int t_end = min(nt_b, t_start + remaining);
+    const int lane = lane_id_fresh();
+    const int head = head_base + (lane & 31);
+    const bool head_ok = head < a.num_heads;
+    const int hi = lane >> 5;
+    // S^T A operand: token lane%32, piece 2*(kc%4) + hi of column block kc/4
+    int k_off_v[4];
+    int k_rope_delta;
+    {
+      const int rg = (lane & 31) >> 3, r = lane & 7;
+      const int sw = piece_swizzle(r, rg);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) k_off_v[j] = rg * NVB * 1024 + (r * 8 + ((2 * j + hi) ^ sw)) * 16;
+      k_rope_delta = OFF_R - rg * (NVB - NRB) * 1024;
+    }
+    // V^T operand of dim block db (ds_read_b64_tr_b16): group g = lane/16,
+    // L = lane%16; read e2 of k-step c covers token 16c + 8e2 + 4(g/2) + L/4,
+    // dims 32db + 16(g%2) + 4(L%4); the column block db/2 and the k-step are
+    // immediate offsets.
+    int v_off[2][2];  // [db & 1][e2]
+    {
+      const int g = lane >> 4, L = lane & 15;
+      const int r = 4 * (g >> 1) + (L >> 2);
+#pragma unroll
+      for (int dbp = 0; dbp < 2; ++dbp)
+#pragma unroll
+        for (int e2 = 0; e2 < 2; ++e2) {
+          const int piece = 4 * dbp + 2 * (g & 1) + ((L & 3) >> 1);
+          v_off[dbp][e2] = e2 * NVB * 1024 + (r * 8 + (piece ^ piece_swizzle(r, e2))) * 16 + 8 * (L & 1);
+        }
+    }
+    const int dma_r = lane >> 3;
+
+    Segment seg;
+    seg.b = b;
+    seg.t0 = t_start;
+    seg.t1 = t_end;
+    {
+      const SegmentSlot ss = segment_slot(a, wr, worker, b, t_start, nt_b, seg_global_off);
+      seg.slot = ss.slot;
+      seg.direct = ss.direct;
+      if (a.fused && !seg.direct && wave == 0 && lane == 0) {
+        int* r = s_pend[b == b_first ? 0 : 1];
+        r[0] = b;
+        r[1] = ss.index;
+        r[2] = ss.count;
+        r[3] = ss.first_slot;
+      }
+    }
+
+    f32x16 acc[NDB];  // O^T: dims 32db.. of this wave's 32 heads
+#pragma unroll
+    for (int d = 0; d < NDB; ++d) acc[d] = (f32x16)0.0f;
+    float m_run = kNoMax;  // base-2 reference max of the lane's head
+    float l_run = 0.0f;    // sum of p over this lane's half of the tokens
+    i16x8 qop[NKQ];  // Q^T of the latent k-chunks (the rope ones are read from OFF_Q)
+
+    const int st0 = 2 * seg.t0;
+    const int st1 = min(2 * seg.t1, (n_b + kSubTokens - 1) / kSubTokens);
+    const int nst = st1 - st0;
+
+    const int32_t* bt_row = PAGED ? a.bt + (int64_t)b * a.bt_sb : a.bt;
+    auto page_fetch = [&](int st) __attribute__((always_inline)) -> int {
+      return s_load_i32(bt_row + page_slot_of<PAGE_UNIFORM>(a, st * kSubTokens));
+    };
+    auto page_ready = [&](int v) __attribute__((always_inline)) -> int {
+      v = s_wait_i32(v);
+      return v < 0 ? 0 : min(v, a.max_page);
+    };
+    // this lane's piece of row 8*wave + lane/8 of a sub-tile that lies in
+    // one page (32 rows of one page: below 2^31 bytes, which the host checks)
+    const uint32_t lane_row_off =
+        (uint32_t)((wave * 8 + dma_r) * (uint32_t)a.kv_s1) + ((lane & 7) ^ piece_swizzle(dma_r, wave)) * 16;
+    auto copy_src = [&](int st, int page) __attribute__((always_inline)) -> const char* {
+      const int tok_base = st * kSubTokens;
+      if (PAGED && PAGE_UNIFORM && tok_base + kSubTokens <= n_b) {
+        const int in_page = tok_base & (a.page_size - 1);
+        return a.kv + (int64_t)page * a.kv_s0 + (int64_t)in_page * a.kv_s1 + lane_row_off;
+      }
+      const int tok = tok_base + wave * 8 + dma_r;
+      int pg = page;
+      if (PAGED && !PAGE_UNIFORM) pg = load_page(a, b, page_slot_of(a, min(tok, n_b - 1)));
+      return a.kv + row_offset<PAGED>(a, b, tok, n_b, pg) + ((lane & 7) ^ piece_swizzle(dma_r, wave)) * 16;
+    };
+    auto copy_one = [&](int k, auto CB, const char* src) __attribute__((always_inline)) {
+      constexpr int cb = decltype(CB)::value;
+      char LDS_AS* dst = cb < NVB ? lds + (k & 3) * VSLOT + (wave * NVB + cb) * 1024
+                                  : lds + OFF_R + (k % RRING) * RSLOT + (wave * NRB + cb - NVB) * 1024;
+      lds_copy16<cb * 128>(src, dst);
+    };
+    auto issue = [&](int st, int page) __attribute__((always_inline)) {
+      const char* src = copy_src(st, page);
+      static_for<NCB>([&](auto CB) __attribute__((always_inline)) { copy_one(st - st0, CB, src); });
+    };
+
+    // A run of NS S^T steps (k-chunks 0..NS-1 of the sub-tile in ring entry
+    // ks, accumulating into sacc, or with two chains into sacc and sacc2, whose
+    // sum is the score tile) followed by NV value steps g = 0..NV-1
+    // (k-step c = g / 16, dim block db = g % 16) of the sub-tile in entry vs,
+    // with the probabilities of k-step c packed in pk[c]. LDS operands are
+    // read PD steps ahead; the wait of every other step counts exactly the
+    // reads issued after those of the step pair. hook(j) runs after step j's
+    // MFMA (softmax pieces, copies, the rescale check).
+    auto run = [&](auto NSC, auto NVC, f32x16& sacc, f32x16& sacc2, const f32x4 (&pk)[2], int ks, int kr, int vs,
+                   auto&& hook)
+                   __attribute__((always_inline)) {
+      constexpr int NS = decltype(NSC)::value, NV = decltype(NVC)::value, NT = NS + NV;
+      const char LDS_AS* kst_v = lds + ks * VSLOT;
+      const char LDS_AS* kvb[4] = {kst_v + k_off_v[0], kst_v + k_off_v[1], kst_v + k_off_v[2], kst_v + k_off_v[3]};
+      const int rope_shift = kr * RSLOT - ks * VSLOT + k_rope_delta;
+      const char LDS_AS* vst = lds + vs * VSLOT;
+      const char LDS_AS* vbase[2][2] = {{vst + v_off[0][0], vst + v_off[0][1]}, {vst + v_off[1][0], vst + v_off[1][1]}};
+      // Q rope rows sit at OFF_Q in the rope ring's layout: the K rope
+      // address plus a uniform shift
+      const int q_shift = OFF_Q + wave * RSLOT - OFF_R - kr * RSLOT;
+      i16x8 kb[NOB], qb[NOB];
+      i16x4 vl[NOB], vh[NOB];
+      auto fetch = [&](auto T) __attribute__((always_inline)) {
+        constexpr int t = decltype(T)::value;
+        if constexpr (t < NS) {
+          constexpr int kc = t, cb = kc >> 2;
+          if constexpr (cb < NVB) {
+            kb[t % (NOB)] = ds_read_b128<cb * 1024>(kvb[kc & 3]);
+          } else {
+            const char LDS_AS* kr = kvb[kc & 3] + rope_shift;
+            kb[t % (NOB)] = ds_read_b128<(cb - NVB) * 1024>(kr);
+            qb[t % (NOB)] = ds_read_b128<(cb - NVB) * 1024>(kr + q_shift);
+          }
+        } else if constexpr (t < NT) {
+          constexpr int g = t - NS, c = g / NDB, db = g % NDB;
+          constexpr int off = c * 2 * NVB * 1024 + (db >> 1) * 1024;
+          vl[t % (NOB)] = ds_read_tr<off>(vbase[db & 1][0]);
+          vh[t % (NOB)] = ds_read_tr<off>(vbase[db & 1][1]);
+        }
+      };
+      static_for<(PD < NT ? PD : NT)>([&](auto T) __attribute__((always_inline)) { fetch(T); });
+      static_for<NT>([&](auto J) __attribute__((always_inline)) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (j + PD < NT) fetch(std::integral_constant<int, j + PD>{});
+        constexpr int r = j % (NOB);
+        if constexpr (j % 2 == 0) {
+          // one wait for the operands of steps j and j + 1
+          constexpr int j2 = j + 1 < NT ? j + 1 : j;
+          constexpr int last = j + PD < NT - 1 ? j + PD : NT - 1;
+          constexpr int after2 = [] {
+            int n = 0;
+            for (int t = j2 + 1; t <= last; ++t) n += own_step_reads<NS, NV>(t);
+            return n;
+          }();
+          static_assert(after2 <= 15, "lgkmcnt range");
+          lgkm_wait<after2>();
+          constexpr int r2 = j2 % (NOB);
+          if constexpr (j < NS && j < NKQ) asm volatile("" : "+v"(kb[r]));
+          else if constexpr (j < NS) asm volatile("" : "+v"(kb[r]), "+v"(qb[r]));
+          else asm volatile("" : "+v"(vl[r]), "+v"(vh[r]));
+          if constexpr (j2 != j) {
+            if constexpr (j2 < NS && j2 < NKQ) asm volatile("" : "+v"(kb[r2]));
+            else if constexpr (j2 < NS) asm volatile("" : "+v"(kb[r2]), "+v"(qb[r2]));
+            else asm volatile("" : "+v"(vl[r2]), "+v"(vh[r2]));
+          }
+        }
+        if constexpr (j < NS) {
+          // SCH = 2: even k-chunks into sacc, odd ones into sacc2, so that no
+          // MFMA waits for the result of the one just before it
+          f32x16& dst = (SCH == 2 && j % 2 == 1) ? sacc2 : sacc;
+          const i16x8& qo = j < NKQ ? qop[j < NKQ ? j : 0] : qb[r];
+          if constexpr (j < SCH)
+            dst = own_mfma_first<DT>(kb[r], qo);
+          else
+            own_mfma_acc<DT>(dst, kb[r], qo);
+        } else {
+          constexpr int g = j - NS, c = g / NDB, db = g % NDB;
+          const i16x4 lo = vl[r], h4 = vh[r];
+          const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], h4[0], h4[1], h4[2], h4[3]};
+          // (the builtin: the compiler sees this MFMA and inserts the wait
+          // states after the VALU writes of pk that it reads)
+          mfma_agpr_acc<DT>(acc[db], vop, __builtin_bit_cast(i16x8, pk[c]));
+        }
+        hook(J);
+      });
+    };
+
+    // O^T columns (one head per lane) times the lane's factor, one block at
+    // a time so the accumulators stay in AGPRs.
+    auto rescale = [&](float alpha) __attribute__((always_inline)) {
+      mfma_agpr_fence(acc[NDB - 1]);
+#pragma unroll
+      for (int d = 0; d < NDB; ++d) {
+        f32x16 t = acc[d];
+        pin_vgpr(t);
+        t *= alpha;
+        acc[d] = t;
+        pin_agpr(acc[d]);
+      }
+    };
+
+    // Online softmax, base 2, with the lazy rescale. Scores stay unscaled: p
+    // = 2^(s * c - m) with c = softmax scale * log2 e, and the max is taken on
+    // s (c > 0) or -s (c < 0). m_run is the reference max the probabilities
+    // of the current sub-tile use. soft_max() looks at the next sub-tile's
+    // scores once their MFMAs are done: masks tokens past the sequence (last
+    // sub-tile only) and moves the reference max, for the whole wave, only
+    // when a score exceeds it by 2^8 (the two token halves of a head then
+    // agree through one lane swap), so p <= 2^8 and O^T rarely needs a
+    // rescale; soft_apply() applies the move at the end of the iteration,
+    // after the current sub-tile's value MFMAs.
+    float m_next = kNoMax, a_next = 1.0f;
+    float mx_part = 0.0f;  // running max of the scores being examined
+    // piece 0: mask, then the max of registers 0-3; pieces 1-3: registers
+    // 4k..4k+3; piece 4: the decision (one piece per step, beside the MFMAs)
+    auto soft_max_piece = [&](f32x16& s, int st, auto K) __attribute__((always_inline)) {
+      constexpr int k = decltype(K)::value;
+      const float c = a.qk_scale_log2;
+      if constexpr (k == 0) {
+        if ((st + 1) * kSubTokens > n_b - lag_wave) {  // tokens past the sequence (for some head)
+          const int ln = lane_id_fresh();
+          const int tok0 = st * kSubTokens + 4 * (ln >> 5);
+          const int lim = n_b - causal_lag(a, head_base + (ln & 31));
+          const float off = c >= 0.0f ? -INFINITY : INFINITY;
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (tok0 + 8 * (r >> 2) + (r & 3) >= lim) s[r] = off;
+        }
+        pin_f16(s);
+      }
+      if constexpr (k < 4) {
+        const float sg = c >= 0.0f ? 1.0f : -1.0f;  // max of s (c > 0) or of -s (c < 0)
+        const float m4 = fmaxf(fmaxf(sg * s[4 * k], sg * s[4 * k + 1]), fmaxf(sg * s[4 * k + 2], sg * s[4 * k + 3]));
+        mx_part = k == 0 ? m4 : fmaxf(mx_part, m4);
+        pin_f1(mx_part);
+      } else {
+        const float mx = mx_part * fabsf(c);
+        m_next = m_run;
+        a_next = 1.0f;
+        if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleLog2) != 0) {
+          float x = mx, y = mx;
+          swap_rows32(x, y);
+          m_next = fmaxf(m_run, fmaxf(x, y));
+          if (m_run != kNoMax) a_next = fast_exp2(m_run - m_next);
+        }
+        pin_f2(m_next, a_next);
+      }
+    };
+    auto soft_max = [&](f32x16& s, int st) __attribute__((always_inline)) {
+      static_for<5>([&](auto K) __attribute__((always_inline)) { soft_max_piece(s, st, K); });
+    };
+    auto soft_apply = [&]() __attribute__((always_inline)) {
+      if (__builtin_amdgcn_ballot_w64(a_next != 1.0f) != 0) rescale(a_next);
+      l_run *= a_next;
+      m_run = m_next;
+    };
+    // p of score r of the current sub-tile, summed into lsum
+    auto soft_exp = [&](f32x16& s, float& lsum, int r) __attribute__((always_inline)) {
+      s[r] = fast_exp2(fmaf(s[r], a.qk_scale_log2, -m_run));  // masked: +-inf * c = -inf -> 0
+      lsum += s[r];
+      pin_f1(lsum);  // summed here, beside the MFMAs, not all at the end
+    };
+
+    // ---- start-up: page ids, Q through LDS, sub-tiles 0 and 1 -------------
+    int pro_page[RING] = {0, 0, 0, 0};
+    if (PAGED && PAGE_UNIFORM) {
+#pragma unroll
+      for (int i = 0; i < RING; ++i) pro_page[i] = page_fetch(st0 + min(i, nst - 1));
+    }
+    stage_q(b);
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int kc = 0; kc < NKQ; ++kc)
+      qop[kc] = *reinterpret_cast<const i16x8 LDS_AS*>(lds + wave * VSLOT + k_off_v[kc & 3] + (kc >> 2) * 1024);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    lds_barrier();  // every wave has its Q^T before the rings are refilled
+    if (PAGED && PAGE_UNIFORM) {
+#pragma unroll
+      for (int i = 0; i < RING; ++i) pro_page[i] = page_ready(pro_page[i]);
+    }
+    issue(st0, pro_page[0]);  // nst >= 1
+    if (nst > 1) {
+      issue(st0 + 1, pro_page[1]);
+      wait_vmcnt<LOADS>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    int next_page = 0;
+    if (b == b_first) phase_stamp(2);
+
+    // ---- prologue: S(0), copies of sub-tile 2 ---------------------------
+    // Copies past the segment's last sub-tile (here and in the last two
+    // iterations with S) read the sequence's last row again into entries no
+    // later step of the segment reads: one loop body serves every iteration
+    // (a loop body instantiated with and without copies leaves the register
+    // allocator no room beside Q^T and O^T).
+    f32x16 sA, sB, sX;  // score tiles of alternate sub-tiles; the second chain's accumulator
+    const char* csrc_n = nullptr;  // copy source (this lane's row) of the next iteration's sub-tile
+    lds_barrier();  // every wave's copies of sub-tile 0 have landed
+    {
+      const char* csrc = nullptr;
+      const f32x4 none[2] = {(f32x4)0.0f, (f32x4)0.0f};
+      run(std::integral_constant<int, NKC>{}, std::integral_constant<int, 0>{}, sA, sX, none, 0, 0, 0,
+          [&](auto J) __attribute__((always_inline)) {
+            constexpr int j = decltype(J)::value;
+            if constexpr (j == 0) csrc = copy_src(st0 + 2, pro_page[2]);
+            static_for<LOADS>([&](auto K) __attribute__((always_inline)) {
+              constexpr int k = decltype(K)::value;
+              if constexpr (k * (NKC - 4) / LOADS + 1 == j) copy_one(2, std::integral_constant<int, k>{}, csrc);
+            });
+          });
+      mfma_vgpr_fence(sA);
+      csrc_n = copy_src(st0 + 3, pro_page[3]);  // iteration 0's copies
+      if constexpr (SCH == 2) {
+        mfma_vgpr_fence(sX);
+        sA += sX;
+      }
+      soft_max(sA, st0);
+      soft_apply();
+    }
+
+    // ---- iterations ---------------------------------------------------------
+    // iteration i < nst - 1: the softmax of sc (sub-tile i) beside S(i+1) into
+    // sn, the copies of sub-tile i+3, then PV(i) and the max of sub-tile i+1
+    auto iteration = [&](const int i, f32x16& sc, f32x16& sn) __attribute__((always_inline)) {
+      // own copies of sub-tile i+1 have landed (those of i+2 may fly)
+      wait_vmcnt<LOADS>();
+      // every wave's copies of sub-tile i+1 have landed and every wave is
+      // done with the entries the copies of sub-tile i+3 refill
+      lds_barrier();
+      const bool stamped = TMLA_STAMPS && b == b_first && (i == kStampIter || i == kStampIter + 1);
+      StampRec st_begin{}, st_mid{}, st_end{};
+      if (stamped) st_begin = stamp_now();
+      // the page id of sub-tile i+4: its load goes out before every counted
+      // LDS read of the run
+      if (PAGED && PAGE_UNIFORM) next_page = page_fetch(st0 + min(i + RING, nst - 1));
+      const int ks = (i + 1) & 3, kr = (i + 1) % RRING, vs = i & 3;
+      const char* const csrc = csrc_n;
+      float lsum = 0.0f;
+      f32x4 pk[2];  // probabilities of sub-tile i, two per register: tokens 0-15, 16-31
+      run(std::integral_constant<int, NKC>{}, std::integral_constant<int, 2 * NDB>{}, sn, sX, pk, ks, kr, vs,
+          [&](auto J) __attribute__((always_inline)) {
+            constexpr int j = decltype(J)::value;
+            if constexpr (j >= E0 && (j - E0) % ES == 0 && (j - E0) / ES < 16) {
+              constexpr int r = (j - E0) / ES;
+              soft_exp(sc, lsum, r);
+              if constexpr (r % 2 == 1) pk[r / 8][(r / 2) % 4] = pack_pair<DT>(sc[r - 1], sc[r]);
+            }
+            static_for<LOADS>([&](auto K) __attribute__((always_inline)) {
+              constexpr int k = decltype(K)::value;
+              if constexpr (CP0 + k * CPS / LOADS == j) copy_one(i + 3, std::integral_constant<int, k>{}, csrc);
+            });
+            if constexpr (j == NKC - 1) {
+              if (stamped) st_mid = stamp_now();
+            }
+            // the scores of sub-tile i+1: their last MFMA issued MX - NKC
+            // steps (and as many MFMAs and operand reads) ago
+            if constexpr (j == MX && SCH == 2) {
+              pin_f16(sX);
+              sn += sX;
+            }
+            if constexpr (j >= MX && j < MX + 5) soft_max_piece(sn, st0 + i + 1, std::integral_constant<int, j - MX>{});
+          });
+      l_run += lsum;
+      soft_apply();
+      // the copy source of the next iteration (sub-tile i+4), computed here
+      // while the last value MFMAs run (every counted LDS read is done, and
+      // the page id requested at the start has arrived)
+      csrc_n = copy_src(st0 + i + 4, (PAGED && PAGE_UNIFORM) ? page_ready(next_page) : 0);
+      if (stamped) {
+        st_end = stamp_now();
+        if (i == kStampIter) {
+          stamp_store(5, st_begin);
+          stamp_store(6, st_mid);
+          stamp_store(7, st_end);
+        } else {
+          stamp_store(8, st_begin);
+        }
+      }
+    };
+    int it = 0;
+    while (it + 1 < nst) {
+      iteration(it, sA, sB);
+      if (++it + 1 >= nst) {
+        sA = sB;  // the last sub-tile's scores
+        break;
+      }
+      iteration(it, sB, sA);
+      ++it;
+    }
+    // last sub-tile of the segment: its softmax, then its value steps
+    {
+      // (every wave's copies of it have landed: the barrier of the last
+      // iteration, or of the prologue, came after their waits)
+      float lsum = 0.0f;
+      f32x4 pk[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        soft_exp(sA, lsum, r);
+        if (r % 2 == 1) pk[r / 8][(r / 2) % 4] = pack_pair<DT>(sA[r - 1], sA[r]);
+      }
+      asm volatile("s_nop 4" : "+v"(pk[0]), "+v"(pk[1]));  // VALU results read by the asm MFMAs below
+      l_run += lsum;
+      run(std::integral_constant<int, 0>{}, std::integral_constant<int, 2 * NDB>{}, sB, sX, pk, 0, 0, (nst - 1) & 3,
+          [](auto) {});
+    }
+    mfma_agpr_fence(acc[NDB - 1]);
+    wait_vmcnt<0>();
+    lds_barrier();  // every wave is done with the rings
+    if (b == b_first) phase_stamp(3);
+
+    // ---- finalize: out = acc / l, lse2 = m + log2(l) ----------------------
+    {
+      const int ln = lane_id_fresh();
+      const int hq = head_base + (ln & 31);
+      const bool hq_ok = hq < a.num_heads;
+      const int h2 = ln >> 5;
+      float l_a = l_run, l_b = l_run;
+      swap_rows32(l_a, l_b);
+      const float l_tot = l_a + l_b;
+      const bool has = l_tot > 0.0f;
+      const float inv = has ? 1.0f / l_tot : 0.0f;
+      const float lse2 = has ? m_run + fast_log2(l_tot) : -INFINITY;
+      // rows of this wave's heads through its own part of the idle rings
+      // (padded pitch: the lanes' 8-byte writes spread over all banks), so
+      // that every global store writes one whole row
+      // (one accumulator block at a time: moved to VGPRs, scaled, rounded
+      // and written before the next block is read)
+      char LDS_AS* obuf = lds + wave * 32 * OPITCH;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        f32x16 t = acc[db];
+        pin_vgpr(t);
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          i16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = Elt<DT>::from_float(t[4 * q4 + e] * inv);
+          const int dim = 32 * db + 8 * q4 + 4 * h2;
+          *reinterpret_cast<i16x4 LDS_AS*>(obuf + (ln & 31) * OPITCH + dim * 2) = v;
+        }
+        asm volatile("" ::: "memory");
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      short* dst;
+      int64_t row_stride;
+      if (seg.direct) {
+        dst = reinterpret_cast<short*>(a.out) + (int64_t)b * a.out_sb + (int64_t)head_base * a.out_sh;
+        row_stride = a.out_sh;
+      } else {
+        dst = a.mid_o + ((int64_t)seg.slot * a.num_heads + head_base) * DV;
+        row_stride = DV;
+      }
+      const int rows = max(0, min(32, a.num_heads - head_base));
+#pragma unroll
+      for (int r0 = 0; r0 < 32; r0 += 8) {
+        i16x8 row[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) row[k] = *reinterpret_cast<const i16x8 LDS_AS*>(obuf + (r0 + k) * OPITCH + ln * 16);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (r0 + k < rows) store_through(reinterpret_cast<i16x8*>(dst + (r0 + k) * row_stride + ln * 8), row[k]);
+      }
+      if (hq_ok && h2 == 0) {
+        if (seg.direct)
+          a.lse[(int64_t)b * a.num_heads + hq] = has ? lse2 * kLn2 : -INFINITY;
+        else
+          store_through_f32(a.mid_lse + (int64_t)seg.slot * a.num_heads + hq, lse2);
+      }
+      // the next segment refills the rings
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      lds_barrier();
+    }
+
+    if (b == b_first) phase_stamp(4);
+    if (a.fused && !seg.direct) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();
+      if (wave == 0 && lane == 0) {
+        const int old = sys_add(a.m_count + (int64_t)b * gridDim.y + blockIdx.y, 1);
+        int* r = s_pend[b == b_first ? 0 : 1];
+        r[4] = old == r[2] - 1;
+      }
+    }
+
+    remaining -= (t_end - t_start);
+    seg_global_off += nt_b;
+    ++b;
+    t_start = 0;
+  }
+
+  if (a.fused) {
+    const CoherentLoads ld{
+        __builtin_amdgcn_make_buffer_rsrc(a.mid_o, 0, a.mid_o_bytes, kBufferWord3),
+        __builtin_amdgcn_make_buffer_rsrc(a.mid_lse, 0, a.mid_o_bytes / 256, kBufferWord3)};
+    fused_merge_tail<DT>(MergeView{a.mid_o, a.mid_lse, a.num_heads, a.out, a.out_sb, a.out_sh, a.lse}, ld,
+                         a.m_count, a.m_done, a.m_flag, a.spin_limit, wave, s_pend, s_msg, 4);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Stage 2: log-sum-exp merge (kernel.py:159-181). One wave per (b, head).
 // ---------------------------------------------------------------------------
 template <int DT, int DV>
@@ -1892,10 +2592,22 @@ hipError_t launch_partial_ring8(const PartialArgs& a, dim3 grid, int nhb, hipStr
   return launch_partial_t<DT, 4, true, true, true>(a, grid, stream);
 }
 
+template <int DT, bool PAGED, bool UNI>
+hipError_t launch_partial_own_t(const PartialArgs& a, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((mla_partial_own_kernel<DT, PAGED, UNI>), grid, dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
 template <int DT>
 hipError_t launch_partial_dt(const PartialArgs& a, dim3 grid, int nhb, hipStream_t stream, bool paged, bool uni) {
   if (nhb == 1) return launch_partial_nw<DT, 1>(a, grid, stream, paged, uni);
   if (nhb == 2) return launch_partial_nw<DT, 2>(a, grid, stream, paged, uni);
+  if (TMLA_OWN_LOOP) {
+    // 128 heads per workgroup: the head-owner loop
+    if (!paged) return launch_partial_own_t<DT, false, false>(a, grid, stream);
+    if (uni) return launch_partial_own_t<DT, true, true>(a, grid, stream);
+    return launch_partial_own_t<DT, true, false>(a, grid, stream);
+  }
   return launch_partial_nw<DT, 4>(a, grid, stream, paged, uni);
 }
 
