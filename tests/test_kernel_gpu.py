@@ -88,6 +88,23 @@ def test_matches_oracle(gpu, num_heads, num_splits, paged):
     check(out, lse, ref_out, ref_lse, seqlens)
 
 
+@pytest.mark.parametrize("num_heads", [20, 128])
+@pytest.mark.parametrize("scale", [-SCALE, -1e-3, 3.0])
+@pytest.mark.parametrize("paged", [False, True])
+def test_scale_sign_and_size(gpu, num_heads, scale, paged):
+    """Negative, tiny and large softmax scales (the reference takes any float,
+    kernel.py:247-248) against the oracle: the 128-head kernel runs a negative
+    scale on negated Q^T, the smaller head blocks take the max of -s."""
+    from triton_mla import mla_decode
+
+    q, kv, seqlens, bt, _ = reference_case(num_heads, paged, torch.bfloat16)
+    ref_out, ref_lse = run_oracle(q, kv, seqlens, bt, scale, torch.bfloat16)
+    out, lse = mla_decode(q.to(gpu), kv.to(gpu), seqlens.to(gpu), None if bt is None else bt.to(gpu),
+                          softmax_scale=scale, return_lse=True)
+    torch.cuda.synchronize()
+    check(out, lse, ref_out, ref_lse, seqlens)
+
+
 def test_default_splits_and_flashmla_layout(gpu):
     from triton_mla import mla_decode
 

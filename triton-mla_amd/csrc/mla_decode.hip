@@ -1699,6 +1699,10 @@ void mla_partial_kernel(PartialArgs a) {
 #ifndef TMLA_OWN_EXTRA_BUF
 #define TMLA_OWN_EXTRA_BUF 0
 #endif
+// 1: a scheduling barrier after every step of the run
+#ifndef TMLA_OWN_SCHED_FENCE
+#define TMLA_OWN_SCHED_FENCE 1
+#endif
 // S^T accumulated in this many chains (1 or 2) over alternate k-chunks
 #ifndef TMLA_OWN_S_CHAINS
 #define TMLA_OWN_S_CHAINS 2
@@ -2023,6 +2027,9 @@ void mla_partial_own_kernel(PartialArgs a) {
           mfma_agpr_acc<DT>(acc[db], vop, __builtin_bit_cast(i16x8, pk[c]));
         }
         hook(J);
+        // the scheduler keeps each step's work in its step (the softmax
+        // pieces and copies spread over the MFMAs as placed, not clustered)
+        if constexpr (TMLA_OWN_SCHED_FENCE) __builtin_amdgcn_sched_barrier(0);
       });
     };
 
@@ -2052,30 +2059,30 @@ void mla_partial_own_kernel(PartialArgs a) {
     // after the current sub-tile's value MFMAs.
     float m_next = kNoMax, a_next = 1.0f;
     float mx_part = 0.0f;  // running max of the scores being examined
+    const float cabs = fabsf(a.qk_scale_log2);
     // piece 0: mask, then the max of registers 0-3; pieces 1-3: registers
-    // 4k..4k+3; piece 4: the decision (one piece per step, beside the MFMAs)
+    // 4k..4k+3; piece 4: the decision (one piece per step, beside the MFMAs).
+    // (A negative softmax scale runs on negated Q^T and |c|, so the scores
+    // are always maximised.)
     auto soft_max_piece = [&](f32x16& s, int st, auto K) __attribute__((always_inline)) {
       constexpr int k = decltype(K)::value;
-      const float c = a.qk_scale_log2;
       if constexpr (k == 0) {
         if ((st + 1) * kSubTokens > n_b - lag_wave) {  // tokens past the sequence (for some head)
           const int ln = lane_id_fresh();
           const int tok0 = st * kSubTokens + 4 * (ln >> 5);
           const int lim = n_b - causal_lag(a, head_base + (ln & 31));
-          const float off = c >= 0.0f ? -INFINITY : INFINITY;
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            if (tok0 + 8 * (r >> 2) + (r & 3) >= lim) s[r] = off;
+            if (tok0 + 8 * (r >> 2) + (r & 3) >= lim) s[r] = -INFINITY;
         }
         pin_f16(s);
       }
       if constexpr (k < 4) {
-        const float sg = c >= 0.0f ? 1.0f : -1.0f;  // max of s (c > 0) or of -s (c < 0)
-        const float m4 = fmaxf(fmaxf(sg * s[4 * k], sg * s[4 * k + 1]), fmaxf(sg * s[4 * k + 2], sg * s[4 * k + 3]));
+        const float m4 = fmaxf(fmaxf(s[4 * k], s[4 * k + 1]), fmaxf(s[4 * k + 2], s[4 * k + 3]));
         mx_part = k == 0 ? m4 : fmaxf(mx_part, m4);
         pin_f1(mx_part);
       } else {
-        const float mx = mx_part * fabsf(c);
+        const float mx = mx_part * cabs;
         m_next = m_run;
         a_next = 1.0f;
         if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleLog2) != 0) {
@@ -2097,7 +2104,7 @@ void mla_partial_own_kernel(PartialArgs a) {
     };
     // p of score r of the current sub-tile, summed into lsum
     auto soft_exp = [&](f32x16& s, float& lsum, int r) __attribute__((always_inline)) {
-      s[r] = fast_exp2(fmaf(s[r], a.qk_scale_log2, -m_run));  // masked: +-inf * c = -inf -> 0
+      s[r] = fast_exp2(fmaf(s[r], cabs, -m_run));  // masked: -inf -> 0
       lsum += s[r];
       pin_f1(lsum);  // summed here, beside the MFMAs, not all at the end
     };
@@ -2113,6 +2120,19 @@ void mla_partial_own_kernel(PartialArgs a) {
 #pragma unroll
     for (int kc = 0; kc < NKQ; ++kc)
       qop[kc] = *reinterpret_cast<const i16x8 LDS_AS*>(lds + wave * VSLOT + k_off_v[kc & 3] + (kc >> 2) * 1024);
+    if (a.qk_scale_log2 < 0.0f) {
+      // negative softmax scale: s * c = (-s) * |c|, with -s from Q^T negated
+      // (a sign flip, exact) in registers and in this wave's Q rope rows
+      const i16x8 sgn = (i16x8)(short)0x8000;
+#pragma unroll
+      for (int kc = 0; kc < NKQ; ++kc) qop[kc] ^= sgn;
+      char LDS_AS* qr = lds + OFF_Q + wave * RSLOT + lane * 16;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        i16x8 v = *reinterpret_cast<const i16x8 LDS_AS*>(qr + 1024 * j);
+        *reinterpret_cast<i16x8 LDS_AS*>(qr + 1024 * j) = v ^ sgn;
+      }
+    }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     lds_barrier();  // every wave has its Q^T before the rings are refilled
     if (PAGED && PAGE_UNIFORM) {
