@@ -71,10 +71,14 @@ size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v
  * once (the counter block and the rounding slack; the same for every call).
  * Every single launch leaves its counters at zero again, and the partials of
  * no call reach that suffix, so later calls of any shape whose
- * tmla_workspace_bytes fits the buffer need nothing. A call whose counters
- * would not fit the block ((2 * batch + slots) * head blocks > 65536) runs as
- * two kernels. No counterpart in the reference (its two launches need no
- * counters).
+ * tmla_workspace_bytes fits the buffer need nothing. The counters are
+ * (2 * batch + slots) int32 per workgroup along the heads of the launched
+ * grid, whose workgroups take 32, 64 or 128 heads (fewer heads per workgroup
+ * when the call would leave compute units idle); a call whose counters
+ * would not fit the block (more than 65536) or whose workgroups would not
+ * all fit the device at once runs as two kernels:
+ * tmla_mla_decode_fused_is_single tells which. No counterpart in the
+ * reference (its two launches need no counters).
  */
 size_t tmla_workspace_zero_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v,
                                  int32_t num_splits, int32_t num_workers);
@@ -95,7 +99,9 @@ size_t tmla_workspace_zero_bytes(int32_t batch, int32_t num_heads, int32_t head_
  *   softmax_scale  multiplies q.k before the softmax (natural-exp domain).
  *   out        [batch, num_heads, head_dim_v] dtype, strides
  *              (out_stride_b, out_stride_h, 1); written for sequences that one
- *              worker completes. lse [batch, num_heads] float32 natural log.
+ *              worker completes. lse [batch, num_heads] float32 natural log,
+ *              or NULL when the caller does not need it (then not written;
+ *              the same holds for every entry point below that takes lse).
  * Page ids are clamped to [0, num_blocks) and page slots to [0, bt_cols) so a
  * malformed table cannot address memory outside the cache. seqlens[b] must
  * not exceed the table's capacity bt_cols * page_size (dense: num_blocks), as

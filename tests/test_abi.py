@@ -48,9 +48,9 @@ COUNTER_BLOCK = 256 * 1024  # the single launch's counter block, the same for ev
 
 
 def _counter_ints(batch, slots, heads):
-    # the single launch's int32 counters: 2 per (sequence, head block) and 1
-    # per (slot, head block), head blocks of up to 128 heads
-    gy = -(-heads // (32 if heads <= 32 else 64 if heads <= 64 else 128))
+    # the single launch's int32 counters: 2 per (sequence, workgroup along the
+    # heads) and 1 per (slot, workgroup); at most, workgroups of 32 heads
+    gy = -(-heads // 32)
     return (2 * batch + slots) * gy
 
 

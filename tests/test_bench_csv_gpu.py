@@ -1,0 +1,36 @@
+"""The triton-mla-bench CSV keeps the reference's column types
+(src/triton_mla/bench.py:17, 93-104): batch, seqlen, heads, num_splits and
+bytes parse as integers and the time columns as floats (empty when a leg did
+not run), for the balanced default and an explicit split count."""
+
+import csv
+import os
+import subprocess
+import sys
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.mark.parametrize("splits", ["balanced", "4"])
+def test_csv_columns_parse(gpu, tmp_path, splits):
+    path = tmp_path / "bench.csv"
+    env = dict(os.environ, PYTHONPATH=os.path.join(ROOT, "triton-mla_amd"))
+    print(f"triton-mla-bench --batch 1 --seqlen 1024 --splits {splits}", flush=True)
+    subprocess.run([sys.executable, "-m", "triton_mla.bench", "--batch", "1", "--seqlen", "1024", "--no-compile",
+                    "--reps", "5", "--splits", splits, "--csv", str(path)], check=True, env=env, timeout=300)
+    rows = list(csv.DictReader(open(path)))
+    assert len(rows) == 1
+    r = rows[0]
+    for k in ("batch", "seqlen", "heads", "num_splits", "bytes"):
+        assert str(int(r[k])) == r[k], (k, r[k])
+    for k in ("triton_us", "eager_us", "compile_us"):
+        if r[k]:
+            float(r[k])
+    assert r["compile_us"] == ""  # --no-compile
+    assert float(r["triton_us"]) > 0
+    # B=1, 1K over the device's compute units: 16 tiles, one per worker
+    assert int(r["num_splits"]) == (16 if splits == "balanced" else 4)

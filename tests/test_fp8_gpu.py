@@ -122,6 +122,12 @@ CASES = {
     "ring_h128_fp16_q_unsplit": (2, 128, [300, 64], 64, "page", False, torch.float16, 1),
     "ring_h48_partial_head_block": (2, 48, [900, 33], 64, "page", False, torch.bfloat16, None),
     "ring_h128_many_workers": (16, 128, [4096] * 16, 64, "page", False, torch.bfloat16, None),
+    # empty sequences on the ring path (out = 0, lse = -inf), balanced and split
+    "ring_h128_empty_and_short": (3, 128, [0, 50, 0], 64, "page", False, torch.bfloat16, None),
+    "ring_h64_empty_splits4": (4, 64, [0, 1, 0, 1300], 32, "tensor", False, torch.bfloat16, 4),
+    # dense fp8 caches wider than 16 heads (one scale per sequence / tensor)
+    "dense_h128_page_scale": (3, 128, [0, 700, 2100], 1, "page", True, torch.bfloat16, None),
+    "dense_h32_tensor_scale_splits2": (2, 32, [333, 64], 1, "tensor", True, torch.float16, 2),
 }
 
 

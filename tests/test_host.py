@@ -71,3 +71,82 @@ def test_torch_reference_functions_match_oracle():
     cache = torch.randn(8, 16, D, generator=g).to(torch.bfloat16)
     got = gather_kv(cache, lens[:2], bt)
     assert np.array_equal(bits(got), oracle.gather_kv(bits(cache), lens[:2].numpy(), bt.numpy()))
+
+
+def _partition_by_simulation(seqlens, workers):
+    """Brute force over the workers: the tiles each one takes (a snapped
+    piece, or a range of the concatenated tiles) and the sequences they
+    touch; returns the largest worker count of one sequence."""
+    tile = 64
+    tiles = [-(-n // tile) if n > 0 else 0 for n in seqlens]
+    total = sum(tiles)
+    if total == 0:
+        return 0
+    c = -(-total // workers)
+    owners = [set() for _ in seqlens]
+    if sum(-(-t // c) for t in tiles) <= workers:
+        w = 0
+        for b, t in enumerate(tiles):
+            for _ in range(-(-t // c)):
+                owners[b].add(w)
+                w += 1
+    else:
+        seq_of_tile = [b for b, t in enumerate(tiles) for _ in range(t)]
+        for w in range(workers):
+            for g in range(w * c, min((w + 1) * c, total)):
+                owners[seq_of_tile[g]].add(w)
+    return max(len(o) for o in owners)
+
+
+@pytest.mark.parametrize("seqlens,workers,expect", [
+    ([8192] * 32, 256, 8),          # headline: snapped, 8 pieces of 16 tiles
+    ([1024], 256, 16),               # one sequence over 16 workers
+    ([16385] * 4, 64, 16),           # snapped (64 pieces == 64 workers)
+    ([16385] * 4, 63, None),         # straddling ranges
+    ([0, 1, 65, 300, 4097, 2000], 19, None),
+    ([0, 0], 256, 0),
+])
+def test_balanced_pieces_matches_the_partition(seqlens, workers, expect):
+    """The integer split count triton-mla-bench writes for the balanced
+    partition equals a brute-force walk of the workers' ranges."""
+    from triton_mla.kernel import balanced_pieces
+
+    got = balanced_pieces(seqlens, workers)
+    assert got == _partition_by_simulation(seqlens, workers)
+    if expect is not None:
+        assert got == expect
+    g = np.random.default_rng(0)
+    for _ in range(200):
+        lens = g.integers(0, 5000, size=int(g.integers(1, 40))).tolist()
+        w = int(g.integers(1, 300))
+        assert balanced_pieces(lens, w) == _partition_by_simulation(lens, w)
+
+
+@pytest.mark.parametrize("made_in_inference", [False, True])
+def test_down_projection_in_inference_mode(made_in_inference):
+    """The step's first GEMM x . [wq_a; wkv_a]^T under torch.inference_mode:
+    parameters made inside it keep no version counter (two GEMMs), parameters
+    made outside it keep the joint weight, refreshed after an in-place change."""
+    import torch.nn.functional as F
+    from triton_mla.model import MLA, MLAConfig
+
+    cfg = MLAConfig(hidden_size=128, num_heads=4, q_lora_rank=64)
+    torch.manual_seed(0)
+    if made_in_inference:
+        with torch.inference_mode():
+            layer = MLA(cfg)
+    else:
+        layer = MLA(cfg)
+    x = torch.randn(3, cfg.hidden_size)
+    with torch.inference_mode():
+        for step in range(2):
+            q_lat, kv = layer._down_proj(x)
+            torch.testing.assert_close(q_lat, F.linear(x, layer.wq_a.weight), rtol=1e-5, atol=1e-5)
+            torch.testing.assert_close(kv, F.linear(x, layer.wkv_a.weight), rtol=1e-5, atol=1e-5)
+            layer.wkv_a.weight.mul_(-2.0)  # in place: the next call must see it
+    # the joint weight kept from inference mode works with autograd on afterwards
+    if not made_in_inference:
+        xg = x.clone().requires_grad_(True)
+        q_lat, kv = layer._down_proj(xg)
+        (q_lat.sum() + kv.sum()).backward()
+        assert xg.grad is not None

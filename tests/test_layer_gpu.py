@@ -256,6 +256,58 @@ def test_project_workspace_shared_across_shapes(gpu):
             assert torch.equal(y, fresh[i]), f"shape {shapes[i]} differs on the shared workspace (round {rep})"
 
 
+def test_project_on_two_streams_and_in_a_graph(gpu):
+    """layer_ops.project keeps a workspace per (device, stream): split
+    contractions of different shapes running at once on two streams give the
+    bits of the same calls run one at a time, a larger call on one stream
+    replaces only that stream's workspace, and a graph captured on a stream
+    with no workspace yet (its own counters cleared inside the graph)
+    reproduces the eager bits on every replay, eager calls between them."""
+    from triton_mla import layer_ops
+
+    gen = torch.Generator().manual_seed(21)
+    shapes = [(16, 1536, 7168), (8, 2048, 4096)]
+    data = []
+    for m, n, k in shapes:
+        x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(gpu)
+        w = (0.02 * torch.randn(n, k, generator=gen)).to(torch.bfloat16).to(gpu)
+        data.append((x, w))
+    serial = [layer_ops.project(x, w) for x, w in data]
+    torch.cuda.synchronize(gpu)
+    streams = [torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream(gpu))
+    outs = [[], []]
+    for rep in range(8):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                outs[i].append(layer_ops.project(*data[i]))
+    torch.cuda.synchronize(gpu)
+    for i in range(2):
+        for rep, y in enumerate(outs[i]):
+            assert torch.equal(y, serial[i]), f"stream {i}, call {rep} differs from the serial result"
+    keys = {k for k in layer_ops._project_ws if k[0] == gpu.index or k[0] == torch.cuda.current_device()}
+    assert {(torch.cuda.current_device(), s.cuda_stream) for s in streams} <= keys
+
+    cap = torch.cuda.Stream(gpu)
+    layer_ops._project_ws.pop((torch.cuda.current_device(), cap.cuda_stream), None)  # pooled streams recur
+    graph = torch.cuda.CUDAGraph()
+    cap.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.graph(graph, stream=cap):
+        g_out = [layer_ops.project(x, w) for x, w in data]
+    assert (torch.cuda.current_device(), cap.cuda_stream) not in layer_ops._project_ws
+    for rep in range(3):
+        for y in g_out:
+            y.zero_()
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        for i in range(2):
+            assert torch.equal(g_out[i], serial[i]), f"replay {rep}, shape {shapes[i]} differs"
+        eager = layer_ops.project(*data[rep % 2])  # eager work between replays
+        torch.cuda.synchronize(gpu)
+        assert torch.equal(eager, serial[rep % 2])
+
+
 def test_project_fp16_and_strided_rows(gpu):
     """fp16 operands, and x / y rows inside wider buffers (row strides larger
     than the row): same product, other rows of the output buffer untouched."""

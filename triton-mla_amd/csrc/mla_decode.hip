@@ -419,14 +419,15 @@ __device__ __forceinline__ void merge_store(const MergeView& mv, int b, int head
   for (int e = 0; e < 8; ++e) o[e] = Elt<DT>::from_float(acc[e] * inv);
   short* orow = reinterpret_cast<short*>(mv.out) + (int64_t)b * mv.out_sb + (int64_t)head * mv.out_sh;
   *reinterpret_cast<i16x8*>(orow + lane * 8) = o;
-  if (lane == 0) mv.lse[(int64_t)b * mv.num_heads + head] = wsum > 0.0f ? (m + fast_log2(wsum)) * kLn2 : -INFINITY;
+  if (lane == 0 && mv.lse)
+    mv.lse[(int64_t)b * mv.num_heads + head] = wsum > 0.0f ? (m + fast_log2(wsum)) * kLn2 : -INFINITY;
 }
 
 // Empty sequence: out = 0, lse = -inf (kernel.py:126-128, 178-181).
 __device__ __forceinline__ void merge_zero(const MergeView& mv, int b, int head, int lane) {
   short* orow = reinterpret_cast<short*>(mv.out) + (int64_t)b * mv.out_sb + (int64_t)head * mv.out_sh;
   *reinterpret_cast<i16x8*>(orow + lane * 8) = (i16x8)0;
-  if (lane == 0) mv.lse[(int64_t)b * mv.num_heads + head] = -INFINITY;
+  if (lane == 0 && mv.lse) mv.lse[(int64_t)b * mv.num_heads + head] = -INFINITY;
 }
 
 // Heads [head, head + nh), nh <= NH, over slots [slot0, slot0 + count),
@@ -994,7 +995,8 @@ void mla_partial_kernel(PartialArgs a) {
       // a whole sub-tile of one page, or the sequence's last sub-tile, whose
       // rows past its end read its last row
       const int tok = min(tok_base + 8 * wave + (ln & 7), n_b - 1);
-      const char* src = a.kv + (int64_t)page * a.kv_s0 + (uint32_t)((tok & (a.page_size - 1)) * (uint32_t)a.kv_s1) +
+      // page_size * kv_s1 may pass 2^32 bytes: the in-page offset in 64 bits
+      const char* src = a.kv + (int64_t)page * a.kv_s0 + (int64_t)(tok & (a.page_size - 1)) * a.kv_s1 +
                         16 * (ln >> 3);
       static_for<4>([&](auto J) __attribute__((always_inline)) {
         constexpr int j = decltype(J)::value;
@@ -1600,8 +1602,9 @@ void mla_partial_kernel(PartialArgs a) {
             if (r0 + k < rows) store_through(reinterpret_cast<i16x8*>(dst + (r0 + k) * row_stride + lane * 8), row[k]);
         }
         if (head_ok && hi == 0) {
-          if (seg.direct)
-            a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
+          if (seg.direct) {
+            if (a.lse) a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
+          }
           else
             store_through_f32(a.mid_lse + (int64_t)seg.slot * a.num_heads + head, lse2);
         }
@@ -2323,8 +2326,9 @@ void mla_partial_own_kernel(PartialArgs a) {
           if (r0 + k < rows) store_through(reinterpret_cast<i16x8*>(dst + (r0 + k) * row_stride + ln * 8), row[k]);
       }
       if (hq_ok && h2 == 0) {
-        if (seg.direct)
-          a.lse[(int64_t)b * a.num_heads + hq] = has ? lse2 * kLn2 : -INFINITY;
+        if (seg.direct) {
+          if (a.lse) a.lse[(int64_t)b * a.num_heads + hq] = has ? lse2 * kLn2 : -INFINITY;
+        }
         else
           store_through_f32(a.mid_lse + (int64_t)seg.slot * a.num_heads + hq, lse2);
       }
@@ -2683,7 +2687,7 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   if (rc != TMLA_OK) return rc;
   if (rope_dim != 64) return fail(TMLA_ERR_UNSUPPORTED, "rope_dim must be 64");
   if (batch == 0) return TMLA_OK;
-  if (!q || !kv || !seqlens || !out || !lse) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!q || !kv || !seqlens || !out) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   if (page_size <= 0 || num_blocks <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "page_size and num_blocks must be > 0");
   const bool paged = block_table != nullptr;
   if (paged && bt_cols <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "block_table needs at least one column");
@@ -2866,7 +2870,7 @@ int tmla_mla_decode_combine(const int32_t* seqlens, int32_t batch, int32_t num_h
   int rc = check_common(c, workspace, workspace_bytes_);
   if (rc != TMLA_OK) return rc;
   if (batch == 0) return TMLA_OK;
-  if (!seqlens || !out || !lse) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!seqlens || !out) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
   CombineArgs a{};
   a.seqlens = seqlens;
   a.batch = batch;

@@ -540,8 +540,9 @@ void mla_partial_fp8_kernel(PartialArgs a) {
       }
       if (wave == 0 && g == 0 && head_ok) {
         const float lse2 = has ? M + fast_log2(L) : -INFINITY;
-        if (ss.direct)
-          a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
+        if (ss.direct) {
+          if (a.lse) a.lse[(int64_t)b * a.num_heads + head] = has ? lse2 * kLn2 : -INFINITY;
+        }
         else
           store_through_f32(a.mid_lse + (int64_t)ss.slot * a.num_heads + head, lse2);
       }

@@ -98,6 +98,29 @@ def load():
     return _lib
 
 
+_held = None
+
+
+def load_gil_held():
+    """The same library through ctypes.PyDLL: its calls keep the GIL held, so
+    the kernels one call launches are never interleaved with launches of
+    another Python thread (used where calls on one stream share a
+    workspace)."""
+    global _held
+    if _held is not None:
+        return _held
+    load()
+    with _lock:
+        if _held is None:
+            lib = ctypes.PyDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _held = lib
+    return _held
+
+
 def check(status: int, what: str) -> None:
     if status != 0:
         msg = load().tmla_last_error().decode(errors="replace")

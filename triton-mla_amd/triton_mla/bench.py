@@ -32,7 +32,7 @@ import torch
 
 from . import workloads
 from .fp8 import dequantize_kv_fp8, quantize_kv_fp8
-from .kernel import DecodeLaunch, _num_sms
+from .kernel import DecodeLaunch, _num_sms, balanced_pieces
 from .reference import mla_decode_torch
 from .timing import Flusher, time_us
 
@@ -106,7 +106,11 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
     if args.kv_fp8 != "none":
         config += f"/fp8-{args.kv_fp8}"
     seqlen = int(inp.seqlens.max())
-    row = [inp.batch, seqlen, args.splits, config, f"{t_hip:.1f}", f"{nbytes / t_hip / 1e6:.2f}",
+    # the CSV's num_splits is an integer, as the reference writes it
+    # (bench.py:98): the uniform count, or for the balanced partition the
+    # largest number of workers one sequence is cut into
+    num_splits = splits if splits is not None else balanced_pieces(inp.seqlens.tolist(), workers)
+    row = [inp.batch, seqlen, num_splits, config, f"{t_hip:.1f}", f"{nbytes / t_hip / 1e6:.2f}",
            f"{flops / t_hip / 1e6:.0f}"]
     if not args.no_eager:
         row.append(f"{t_eager:.1f}")
@@ -115,7 +119,7 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
     print("| " + " | ".join(str(c) for c in row) + " |", flush=True)
     if writer:
         writer.writerow({"gpu": gpu, "batch": inp.batch, "seqlen": seqlen, "heads": inp.heads,
-                         "num_splits": args.splits, "config": config, "bytes": nbytes, "triton_us": t_hip,
+                         "num_splits": num_splits, "config": config, "bytes": nbytes, "triton_us": t_hip,
                          "eager_us": t_eager, "compile_us": t_compile})
 
 

@@ -37,11 +37,18 @@ def _cdiv(a: int, b: int) -> int:
     return -(-a // b)
 
 
+_CU_COUNT = {}  # device index -> compute units
+
+
 def _num_sms(device) -> int:
     """Compute units of ``device`` (kernel.py:184-187; 132 off-GPU as there)."""
     device = torch.device(device)
     if device.type == "cuda":
-        return torch.cuda.get_device_properties(device).multi_processor_count
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        n = _CU_COUNT.get(idx)
+        if n is None:
+            n = _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+        return n
     return 132
 
 
@@ -61,11 +68,62 @@ def get_num_splits(batch, num_heads, max_seqlen, num_sms, min_tokens_per_split=1
     return 1 << (splits.bit_length() - 1)
 
 
+def balanced_pieces(seqlens, num_workers: int) -> int:
+    """Largest number of workers the balanced partition (``num_splits=None``)
+    gives one sequence of ``seqlens`` (host integers), i.e. its split count.
+
+    Host restatement of the device planner (csrc/decode_common.h work_range /
+    segment_slot): the T = sum cdiv(n, 64) tiles are cut into ranges of
+    c = cdiv(T, num_workers) tiles; when the sequences cut into pieces of at
+    most c tiles make no more pieces than workers, each sequence has
+    cdiv(tiles, c) pieces ("snapped"), otherwise a sequence at global tile
+    offset o is covered by the workers o // c .. (o + tiles - 1) // c.
+    0 when every sequence is empty.
+    """
+    tiles = [_cdiv(int(n), 64) if int(n) > 0 else 0 for n in seqlens]
+    total = sum(tiles)
+    if total == 0 or num_workers <= 0:
+        return 0
+    c = _cdiv(total, num_workers)
+    if sum(_cdiv(t, c) for t in tiles) <= num_workers:
+        return max(_cdiv(t, c) for t in tiles)
+    best, off = 0, 0
+    for t in tiles:
+        if t:
+            best = max(best, (off + t - 1) // c - off // c + 1)
+        off += t
+    return best
+
+
 # The form mla_decode runs when single_launch is None: False = the two
 # kernels of the reference's scheme (partial, then combine), True = the single
 # launch (the merge inside the partial kernel, same bits) whenever its
 # workgroups fit on the device at once.
 DEFAULT_SINGLE_LAUNCH = False
+
+
+# (device, shape, ...) -> (workspace bytes, counter bytes to clear, single launch)
+_PLANS = {}
+
+
+class _OnDevice:
+    """torch.cuda.device(idx) only when idx is not already current (entering
+    the context costs more than the launch it guards)."""
+
+    __slots__ = ("idx", "ctx")
+
+    def __init__(self, idx):
+        self.idx = idx
+        self.ctx = None
+
+    def __enter__(self):
+        if torch.cuda.current_device() != self.idx:
+            self.ctx = torch.cuda.device(self.idx)
+            self.ctx.__enter__()
+
+    def __exit__(self, *exc):
+        if self.ctx is not None:
+            self.ctx.__exit__(*exc)
 
 
 def _aligned(t: torch.Tensor, elems: int = 8) -> bool:
@@ -179,10 +237,12 @@ class DecodeLaunch:
             raise ValueError("kv_cache holds no tokens")
         if fp8 and block_table is not None and page_size % 16 != 0:
             raise NotImplementedError("an fp8 kv_cache needs pages of a multiple of 16 tokens")
+        # a fresh copy (contiguous() keeps a contiguous view at its unaligned
+        # address)
         if not _aligned(q):
-            q = q.contiguous()
+            q = q.clone(memory_format=torch.contiguous_format)
         if not _aligned(kv_cache, 16 if fp8 else 8):
-            kv_cache = kv_cache.contiguous()
+            kv_cache = kv_cache.clone(memory_format=torch.contiguous_format)
         scale_args = ()
         if fp8:
             lead = kv_cache.shape[0]
@@ -194,23 +254,32 @@ class DecodeLaunch:
         self.splits = num_splits if num_splits is not None else 0
         # balanced partition: one worker per compute unit unless asked otherwise
         self.workers = 0 if num_splits is not None else int(num_workers or _num_sms(device))
-        self.ws_bytes = self.lib.tmla_workspace_bytes(batch, vheads, head_dim_v, self.splits, self.workers)
+        dev_idx = device.index if device.index is not None else torch.cuda.current_device()
+        self._dev_idx = dev_idx
+        # The library's answers for this shape (workspace size, the counter
+        # block the single launch needs cleared, whether it runs as one
+        # launch) depend on the shape and device only: asked once per shape.
+        # run(single_launch=True) merges inside the partial kernel when all of
+        # its workgroups fit on the device at once, one per CU.
+        capacity = (block_table.shape[1] * page_size) if block_table is not None else num_blocks
+        key = (dev_idx, batch, vheads, head_dim_v, self.splits, self.workers, capacity, fp8, id(self.lib))
+        plan = _PLANS.get(key)
+        if plan is None:
+            ws = self.lib.tmla_workspace_bytes(batch, vheads, head_dim_v, self.splits, self.workers)
+            zero = min(self.lib.tmla_workspace_zero_bytes(batch, vheads, head_dim_v, self.splits, self.workers), ws)
+            fused = not fp8 and bool(self.lib.tmla_mla_decode_fused_is_single(
+                batch, vheads, head_dim_v, self.splits, self.workers, capacity, dev_idx))
+            if len(_PLANS) > 4096:
+                _PLANS.clear()
+            plan = _PLANS[key] = (ws, zero, fused)
+        self.ws_bytes, self._zero_bytes, self.fused = plan
         # Uninitialised like the reference's buffers (kernel.py:268-271): the
         # two-kernel form writes every byte it reads. Only the single launch's
         # merge counters (a small block at the end) must start at zero; they
         # are cleared before the first single launch and every launch leaves
         # them at zero again.
         self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=device)
-        self._zero_bytes = min(self.lib.tmla_workspace_zero_bytes(batch, vheads, head_dim_v, self.splits,
-                                                                  self.workers), self.ws_bytes)
         self._counters_clear = False
-        # run(single_launch=True) merges inside the partial kernel (one launch)
-        # when all of its workgroups fit on the device at once, one per CU: the
-        # library's own decision for these arguments
-        capacity = (block_table.shape[1] * page_size) if block_table is not None else num_blocks
-        self.fused = not fp8 and bool(self.lib.tmla_mla_decode_fused_is_single(
-            batch, vheads, head_dim_v, self.splits, self.workers, capacity,
-            device.index if device.index is not None else torch.cuda.current_device()))
         out_sh = self.out.stride(-2)  # one output row per (query token, head)
         self._partial_args = (
             q.data_ptr(), q.stride(0), q.stride(1),
@@ -239,7 +308,7 @@ class DecodeLaunch:
         if self.q_len > 1:
             raise NotImplementedError("multi-token queries run both stages at once (run())")
         if self.batch:
-            with torch.cuda.device(self.device):
+            with _OnDevice(self._dev_idx):
                 if self.fp8:
                     _native.check(self.lib.tmla_mla_decode_fp8_partial(*self._fp8_partial_args, self._stream()),
                                   "tmla_mla_decode_fp8_partial")
@@ -252,7 +321,7 @@ class DecodeLaunch:
         if self.q_len > 1:
             raise NotImplementedError("multi-token queries run both stages at once (run())")
         if self.batch:
-            with torch.cuda.device(self.device):
+            with _OnDevice(self._dev_idx):
                 _native.check(self.lib.tmla_mla_decode_combine(*self._combine_args, self._stream()),
                               "tmla_mla_decode_combine")
 
@@ -269,16 +338,16 @@ class DecodeLaunch:
         its share over (< 0: the library's default). An fp8 cache always
         runs the two kernels."""
         if self.batch and self.fp8:
-            with torch.cuda.device(self.device):
+            with _OnDevice(self._dev_idx):
                 _native.check(self.lib.tmla_mla_decode_fp8(*self._fp8_args, self._stream()), "tmla_mla_decode_fp8")
         elif self.batch and self.q_len > 1:
-            with torch.cuda.device(self.device):
+            with _OnDevice(self._dev_idx):
                 if single_launch:
                     self._clear_counters()
                 _native.check(self.lib.tmla_mla_decode_causal(*self._causal_args, int(bool(single_launch)),
                                                               self._stream()), "tmla_mla_decode_causal")
         elif self.batch:
-            with torch.cuda.device(self.device):
+            with _OnDevice(self._dev_idx):
                 if single_launch:
                     self._clear_counters()
                     _native.check(self.lib.tmla_mla_decode_fused(*self._partial_args, int(spin_limit),
@@ -338,9 +407,124 @@ def mla_decode(
         out [batch, num_heads, head_dim_v] in q.dtype (and lse [batch,
         num_heads] float32).
     """
+    single = DEFAULT_SINGLE_LAUNCH if single_launch is None else bool(single_launch)
+    if not single and kv_scale is None:
+        res = _fast_call(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits, return_lse)
+        if res is not None:
+            return res if return_lse else res[0]
     call = DecodeLaunch(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits,
                         kv_scale=kv_scale)
-    out, lse = call.run(DEFAULT_SINGLE_LAUNCH if single_launch is None else single_launch)
+    out, lse = call.run(single)
     if return_lse:
         return out, lse
     return out
+
+
+class _CallShape:
+    """What a two-kernel ``mla_decode`` call derives from its arguments'
+    shapes, strides, dtypes and device alone: the validated geometry and the
+    launch's constant arguments. Built by a full DecodeLaunch the first time
+    a shape is seen, so every assertion of kernel.py:235-271 has run on it;
+    later calls of the same shape only read addresses and allocate."""
+
+    __slots__ = ("dev_idx", "device", "dtype", "out_shape", "lse_shape", "ws_alloc", "ws_bytes",
+                 "a_q", "a_kv", "a_bt", "a_mid", "a_out", "fn")
+
+
+_SHAPES = {}
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or \
+    (lambda idx: torch.cuda.current_stream(idx).cuda_stream)
+_capturing = getattr(torch._C, "_cuda_isCurrentStreamCapturing", None) or torch.cuda.is_current_stream_capturing
+_current_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+
+# (device index, stream) -> workspace of the two-kernel calls that Python
+# launches on that stream. The two kernels write every workspace byte they
+# read, and calls on one stream run in order, so one buffer serves them all;
+# a larger need replaces it (the caching allocator hands the old one out again
+# only to work queued after the calls that use it). The library is called
+# with the GIL held, so two Python threads on one stream cannot interleave
+# their calls' kernels. Under graph capture each call takes its own workspace
+# from the graph's memory instead, so replays share nothing with eager calls.
+_STREAM_WS = {}
+
+
+def _workspace(shape, stream):
+    if _capturing():
+        return torch.empty(shape.ws_alloc, dtype=torch.uint8, device=shape.device)
+    key = (shape.dev_idx, stream)
+    ws = _STREAM_WS.get(key)
+    if ws is None or ws.numel() < shape.ws_alloc:
+        ws = _STREAM_WS[key] = torch.empty(shape.ws_alloc, dtype=torch.uint8, device=shape.device)
+    return ws
+
+
+def _fast_call(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits, want_lse):
+    """Two-kernel decode of a shape seen before: (out, lse or None), or None
+    to take the full path.
+
+    Taken only when nothing would be copied or converted: q and the cache 3-D
+    (or with the singleton kv-head dim) and 16-byte aligned, cache_seqlens
+    (and block_table) int32 on q's device, the device current. The lse is
+    neither allocated nor written unless asked for."""
+    try:
+        bt_key = None if block_table is None else (block_table.dtype, block_table.get_device(), block_table.shape,
+                                                   block_table.stride())
+        key = (q.shape, q.stride(), q.dtype, q.get_device(), kv_cache.shape, kv_cache.stride(), kv_cache.dtype,
+               kv_cache.get_device(), cache_seqlens.dtype, cache_seqlens.get_device(), cache_seqlens.shape,
+               cache_seqlens.stride(), bt_key, head_dim_v, softmax_scale, num_splits)
+    except (AttributeError, TypeError):
+        return None
+    shape = _SHAPES.get(key)
+    qp, kp = q.data_ptr(), kv_cache.data_ptr()
+    if (qp | kp) & 15:
+        return None
+    if shape is None:
+        shape = _learn_shape(key, q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale,
+                             num_splits)
+    if not shape or _current_device() != shape.dev_idx:
+        return None
+    out = q.new_empty(shape.out_shape)
+    lse = q.new_empty(shape.lse_shape, dtype=torch.float32) if want_lse else None
+    stream = _raw_stream(shape.dev_idx)
+    ws = _workspace(shape, stream)
+    status = shape.fn(qp, *shape.a_q, kp, *shape.a_kv, None if block_table is None else block_table.data_ptr(),
+                      *shape.a_bt, cache_seqlens.data_ptr(), *shape.a_mid, out.data_ptr(), *shape.a_out,
+                      None if lse is None else lse.data_ptr(), ws.data_ptr(), shape.ws_bytes, stream)
+    if status:
+        _native.check(status, "tmla_mla_decode")
+    return out, lse
+
+
+def _learn_shape(key, q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits):
+    """Validate one call of a new shape through DecodeLaunch and keep its
+    constant arguments; False (kept too) when the fast path does not apply
+    to the shape. q and kv_cache are 16-byte aligned here."""
+    shape = False
+    if q.dim() == 3 and kv_cache.dtype in _DTYPES and cache_seqlens.dtype == torch.int32 \
+            and cache_seqlens.device == q.device and cache_seqlens.is_contiguous() \
+            and (block_table is None or (block_table.dtype == torch.int32 and block_table.device == q.device
+                                         and block_table.dim() == 2 and block_table.stride(-1) == 1)):
+        call = DecodeLaunch(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits)
+        # no copies made (strides the kernels take as given), one query token
+        if call.batch and call.q_len == 1 and not call.fp8 and call._keep[0] is q \
+                and call._keep[1].data_ptr() == kv_cache.data_ptr():
+            shape = _shape_of(call, q.dtype)
+    if len(_SHAPES) > 1024:
+        _SHAPES.clear()
+    _SHAPES[key] = shape
+    return shape
+
+
+def _shape_of(call, dtype):
+    a = call._partial_args
+    shape = _CallShape()
+    shape.dev_idx, shape.device, shape.dtype = call._dev_idx, call.device, dtype
+    shape.out_shape, shape.lse_shape = tuple(call.out.shape), tuple(call.lse.shape)
+    shape.ws_alloc, shape.ws_bytes = call.workspace.numel(), call.ws_bytes
+    # _partial_args: q ptr, q strides (2), cache ptr, cache strides, blocks,
+    # page size (4), table ptr, table stride, width (2), seqlens ptr, batch ..
+    # workers (8), out ptr, out strides (2), lse ptr, workspace ptr, its size
+    shape.a_q, shape.a_kv, shape.a_bt = a[1:3], a[4:8], a[9:11]
+    shape.a_mid, shape.a_out = a[12:20], a[21:23]
+    shape.fn = _native.load_gil_held().tmla_mla_decode
+    return shape

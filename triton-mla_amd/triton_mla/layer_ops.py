@@ -155,19 +155,40 @@ def project_fits(x, weight):
     return x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0
 
 
-_project_ws = {}  # device index -> zero-filled workspace of the split contractions (grown on demand)
+# (device index, stream) -> zero-filled workspace of the split contractions
+_project_ws = {}
+# workspaces replaced by larger ones: never freed, since graphs captured
+# while they were current still read and write them
+_project_retired = []
+_PROJECT_COUNTER_BYTES = 64 * 1024  # the counter block at the workspace's start
 
 
-def _project_workspace(dev, nbytes):
-    """A zero-filled workspace of at least nbytes on dev, kept for later calls
-    (each call leaves its counters at zero). A larger buffer replaces a
-    smaller one; the old one stays valid for work already queued, since the
-    caching allocator reuses it only after the stream's earlier work."""
+def _project_workspace(dev, stream, nbytes):
+    """A workspace of at least nbytes whose counter block is zero, for a
+    projection on ``stream`` of ``dev``.
+
+    Eager calls keep one per (device, stream), zero-filled once: every call
+    leaves its counters at zero again, and calls on one stream run in order,
+    so the next call finds them cleared. A larger need replaces it with a
+    larger one. Under graph capture the stream's kept workspace is used when
+    there is one large enough (the graph then shares it: replay such a graph
+    on the stream it was captured on). Otherwise the captured call gets a
+    workspace of its own from the graph's memory, its counters cleared by a
+    fill kernel inside the graph: memory allocated during capture holds
+    nothing until the graph replays, so no eager call may find it."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    buf = _project_ws.get(idx)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
-        _project_ws[idx] = buf
+    key = (idx, stream)
+    buf = _project_ws.get(key)
+    if buf is not None and buf.numel() >= nbytes:
+        return buf
+    if torch.cuda.is_current_stream_capturing():
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        buf[:min(nbytes, _PROJECT_COUNTER_BYTES)].zero_()
+        return buf
+    if buf is not None:
+        _project_retired.append(buf)
+    buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+    _project_ws[key] = buf
     return buf
 
 
@@ -183,10 +204,11 @@ def project(x, weight):
     y = torch.empty(m, n, dtype=x.dtype, device=dev)
     lib = _native.load()
     need = lib.tmla_mla_project_workspace_bytes(m, n, k)
-    ws = _project_workspace(dev, need) if need else None
     with torch.cuda.device(dev):
+        stream = _stream(dev)
+        ws = _project_workspace(dev, stream, need) if need else None
         _native.check(lib.tmla_mla_project(
             x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), m, n, k, _native.DTYPE_CODE[x.dtype],
             y.data_ptr(), y.stride(0), None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
-            _stream(dev)), "tmla_mla_project")
+            stream), "tmla_mla_project")
     return y

@@ -151,9 +151,7 @@ class MLA(nn.Module):
             # the HIP glue runs in the layer's 16-bit dtype; other dtype mixes
             # take the reference's torch glue, which casts (model.py:108-124)
             return self.forward_torch_glue(x, kv_cache, cache_seqlens, block_table, num_splits)
-        # wq_a and wkv_a read the same rows: one GEMM over both weights
-        down = F.linear(x, self._down_weight())  # [B, q_lora_rank + rank + rope]
-        q_lat, kv_proj = down[:, :cfg.q_lora_rank], down[:, cfg.q_lora_rank:]
+        q_lat, kv_proj = self._down_proj(x)  # [B, q_lora_rank], [B, rank + rope]
         q_lat = layer_ops.rms_norm(q_lat, self.q_norm.weight, self.q_norm.eps)
         q_proj = self._linear(self.wq_b, q_lat)  # [B, H * (nope + rope)]
         # RMSNorm(c_kv), RoPE(k_pe) and the paged append (model.py:80-94)
@@ -178,17 +176,23 @@ class MLA(nn.Module):
             return layer_ops.project(x, layer.weight)
         return layer(x)
 
-    def _down_weight(self):
-        """[wq_a; wkv_a] as one [q_lora_rank + rank + rope, hidden] weight,
-        rebuilt when either parameter is replaced or changed in place."""
+    def _down_proj(self, x):
+        """x . wq_a^T and x . wkv_a^T. Both read the same rows, so they run as
+        one GEMM over [wq_a; wkv_a], concatenated once and kept while neither
+        parameter is replaced or changed in place (data pointers and version
+        counters). Inference tensors keep no version counter to tell an
+        in-place change by: for them the two GEMMs run separately."""
         wa, wk = self.wq_a.weight, self.wkv_a.weight
+        if wa.is_inference() or wk.is_inference():
+            return F.linear(x, wa), F.linear(x, wk)
         key = (wa.data_ptr(), wa._version, wk.data_ptr(), wk._version, wa.dtype, wa.device)
         cached = getattr(self, "_down_cache", None)
         if cached is None or cached[0] != key:
-            with torch.no_grad():
+            with torch.no_grad(), torch.inference_mode(False):  # a plain tensor, usable in any mode
                 cached = (key, torch.cat([wa.detach(), wk.detach()], dim=0))
             self._down_cache = cached
-        return cached[1]
+        down = F.linear(x, cached[1])
+        return down[:, :wa.shape[0]], down[:, wa.shape[0]:]
 
     def forward_torch_glue(self, x, kv_cache, cache_seqlens, block_table=None, num_splits=None):
         """The absorbed step with the reference's torch glue around the HIP
