@@ -239,12 +239,13 @@ constexpr bool pass_has_pv(int t, int NV, int PVOFF, int PVS) {
   return t >= PVOFF && (t - PVOFF) % PVS == 0 && (t - PVOFF) / PVS < NV;
 }
 
-// LDS reads issued by fetch(t) of a pass (one K operand per S step; on the
-// PV steps, two V^T halves at the first head block of a PV column block and
-// one P^T operand at the first column block of a (token half, head block)).
-template <int NS, int NV, int PV0, int NHB, int PVOFF, int PVS>
+// LDS reads issued by fetch(t) of a pass (one K operand per S step, and a
+// Q^T operand beside it for k-chunks SLO + t >= QR0; on the PV steps, two
+// V^T halves at the first head block of a PV column block and one P^T
+// operand at the first column block of a (token half, head block)).
+template <int NS, int NV, int PV0, int NHB, int PVOFF, int PVS, int SLO, int QR0>
 constexpr int pass_reads(int t) {
-  int n = t < NS ? 1 : 0;
+  int n = t < NS ? (SLO + t >= QR0 ? 2 : 1) : 0;
   if (pass_has_pv(t, NV, PVOFF, PVS)) {
     const int g = PV0 + (t - PVOFF) / PVS;
     n += (g % NHB == 0 ? 2 : 0) + ((g % (4 * NHB)) / NHB == 0 ? 1 : 0);
@@ -738,7 +739,14 @@ void mla_partial_kernel(PartialArgs a) {
   constexpr int OFF_S = OFF_R + kRopeStages * RSLOT;
   constexpr int OFF_P = OFF_S + (F8 ? 2 * STG : 0);
   constexpr int OFF_A = OFF_P + 2 * PSLOT;
-  constexpr int SMEM = OFF_A + 2 * ASLOT;
+  // With two S waves (64 heads), the rope rows of Q stay in LDS for the
+  // whole kernel (RSLOT per S wave) and S reads their Q^T operands from there
+  // beside the K rope operands: 16 VGPRs fewer than Q^T all in registers,
+  // which the 64-head accumulators need.
+  constexpr bool QR = NHB == 2 && TMLA_Q_LDS;
+  constexpr int NKQ = QR ? 4 * NVB : NKC;  // k-chunks of Q^T held in VGPRs
+  constexpr int OFF_QR = OFF_A + 2 * ASLOT;
+  constexpr int SMEM = OFF_QR + (QR ? NHB * RSLOT : 0);
   constexpr int RG_PER_WAVE = 4 / NW;
   constexpr int LOADS = RG_PER_WAVE * NCB;  // DMA instructions per wave per sub-tile
   constexpr int OPITCH = DV * 2 + 16;        // output staging row pitch (bytes)
@@ -783,7 +791,9 @@ void mla_partial_kernel(PartialArgs a) {
   // wave 3's rows in the staging area and the rope rows of waves 2 and 3 in P
   // buffer 0, which holds two rope entries when all four waves run S.
   const int qv = wave < VST ? wave * VSLOT : OFF_S;
-  const int qrope = s_owner ? (wave < kRopeStages ? OFF_R + wave * RSLOT : OFF_P + (wave - kRopeStages) * RSLOT) : 0;
+  const int qrope = !s_owner ? 0
+                    : QR ? OFF_QR + wave * RSLOT
+                         : (wave < kRopeStages ? OFF_R + wave * RSLOT : OFF_P + (wave - kRopeStages) * RSLOT);
   static_assert(!F8 || NHB < 4 || PSLOT >= 2 * RSLOT, "Q rope staging in P buffer 0");
   auto stage_q = [&](int bq) __attribute__((always_inline)) {
     const int ln = lane_id_fresh();
@@ -851,29 +861,34 @@ void mla_partial_kernel(PartialArgs a) {
     // two rings differ only in the row-group stride)
     int k_off_v[4];
     int k_rope_delta;
-    {
-      const int rg = (lane & 31) >> 3, r = lane & 7;
-      const int sw = piece_swizzle(r, rg);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) k_off_v[j] = rg * NVB * 1024 + (r * 8 + ((2 * j + hi) ^ sw)) * 16;
-      k_rope_delta = OFF_R - rg * (NVB - NRB) * 1024;
-    }
     // V^T operand via ds_read_b64_tr_b16: group g = lane/16, L = lane%16;
     // read e2 covers tokens 16c + 8e2 + 4(g/2) + L/4, dims 32db + 16(g%2) + 4(L%4).
     // This wave's dims start at block column (wave * NDBW / 2).
     int v_off[2][2];  // [db&1][e2]
-    {
-      const int g = lane >> 4, L = lane & 15;
-      const int r = 4 * (g >> 1) + (L >> 2);
+    // (set again before the sub-tile loop of an fp8 segment, from a fresh
+    // lane id, so that they need not stay live across its start-up)
+    auto set_lane_offsets = [&](int ln) __attribute__((always_inline)) {
+      {
+        const int rg = (ln & 31) >> 3, r = ln & 7;
+        const int sw = piece_swizzle(r, rg);
 #pragma unroll
-      for (int dbp = 0; dbp < 2; ++dbp)
+        for (int j = 0; j < 4; ++j) k_off_v[j] = rg * NVB * 1024 + (r * 8 + ((2 * j + (ln >> 5)) ^ sw)) * 16;
+        k_rope_delta = OFF_R - rg * (NVB - NRB) * 1024;
+      }
+      {
+        const int g = ln >> 4, L = ln & 15;
+        const int r = 4 * (g >> 1) + (L >> 2);
 #pragma unroll
-        for (int e2 = 0; e2 < 2; ++e2) {
-          const int piece = 4 * dbp + 2 * (g & 1) + ((L & 3) >> 1);
-          v_off[dbp][e2] = e2 * NVB * 1024 + wave * (NDBW / 2) * 1024 +
-                           (r * 8 + (piece ^ piece_swizzle(r, e2))) * 16 + 8 * (L & 1);
-        }
-    }
+        for (int dbp = 0; dbp < 2; ++dbp)
+#pragma unroll
+          for (int e2 = 0; e2 < 2; ++e2) {
+            const int piece = 4 * dbp + 2 * (g & 1) + ((L & 3) >> 1);
+            v_off[dbp][e2] = e2 * NVB * 1024 + wave * (NDBW / 2) * 1024 +
+                             (r * 8 + (piece ^ piece_swizzle(r, e2))) * 16 + 8 * (L & 1);
+          }
+      }
+    };
+    set_lane_offsets(lane);
     // DMA: this lane copies, for each of its wave's row-groups, the piece
     // (lane%8) ^ swizzle of token row 8rg + lane/8.
     const int dma_r = lane >> 3;
@@ -906,7 +921,7 @@ void mla_partial_kernel(PartialArgs a) {
     // so that p = exp2(s * c - m) of a masked score (s = -inf) is 0 even then
     float m_run = kNoMax;
     float l_run = 0.0f;       // sum of p over this lane's half of the tokens
-    i16x8 qop[NKC];           // Q^T operands (B of S^T = K . Q^T), loaded below
+    i16x8 qop[NKQ];           // Q^T operands (B of S^T = K . Q^T), loaded below
     i16x8 pop[2][NHB];        // P^T operands of the sub-tile in PV: [c][hb]
 
     // sub-tiles of 32 tokens; a trailing fully-invalid half tile is skipped
@@ -1051,7 +1066,9 @@ void mla_partial_kernel(PartialArgs a) {
     // after its own. hook(step) runs after each step's MFMAs (copies of a
     // later sub-tile, the rescale check, softmax pieces), so its VALU and
     // memory work overlaps them.
-    constexpr int PD = TMLA_READ_AHEAD;
+    // (two steps for the fp8 ring with 64 heads, whose widening leaves too
+    // few registers for three steps of operands beside Q^T)
+    constexpr int PD = F8 && NHB == 2 && TMLA_READ_AHEAD > 2 ? 2 : TMLA_READ_AHEAD;
     constexpr int SPC = NDBW * NHB;    // PV steps per token half
     // PV steps beside S (pass 1); the rest run beside the softmax (pass 2)
     constexpr int PV_SPLIT = NHB * TMLA_PV1_EIGHTHS;
@@ -1085,7 +1102,13 @@ void mla_partial_kernel(PartialArgs a) {
       const char LDS_AS* vbase[2][2] = {{vst + v_off[0][0], vst + v_off[0][1]},
                                         {vst + v_off[1][0], vst + v_off[1][1]}};
       const char LDS_AS* pbase = pst + lane * 16;
+      // Q^T rope operands (QR): the K rope operand's offsets in this wave's
+      // Q rope rows
+      const int q_shift = qrope - OFF_R + k_rope_delta;
+      const char LDS_AS* qrb[4] = {lds + k_off_v[0] + q_shift, lds + k_off_v[1] + q_shift,
+                                   lds + k_off_v[2] + q_shift, lds + k_off_v[3] + q_shift};
       i16x8 kb[PD + 1];
+      i16x8 qb[PD + 1];
       i16x4 vl[NDBW * 2], vh[NDBW * 2];  // indexed by V^T operand id c * NDBW + j4
       auto fetch = [&](auto T) __attribute__((always_inline)) {
         constexpr int t = decltype(T)::value;
@@ -1095,6 +1118,7 @@ void mla_partial_kernel(PartialArgs a) {
             kb[t % (PD + 1)] = ds_read_b128<cb * 1024>(kvb[kc & 3]);
           else
             kb[t % (PD + 1)] = ds_read_b128<(cb - NVB) * 1024>(krb[kc & 3]);
+          if constexpr (kc >= NKQ) qb[t % (PD + 1)] = ds_read_b128<(cb - NVB) * 1024>(qrb[kc & 3]);
         }
         if constexpr (pass_has_pv(t, NV, PVOFF, PVS)) {
           constexpr int g = PV0 + (t - PVOFF) / PVS, c = g / SPC, j4 = (g % SPC) / NHB, hb = g % NHB;
@@ -1115,7 +1139,7 @@ void mla_partial_kernel(PartialArgs a) {
         constexpr int last = (j + ahead < NSTEPS - 1) ? j + ahead : NSTEPS - 1;
         constexpr int after = [] {
           int n = 0;
-          for (int t = j + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NHB, PVOFF, PVS>(t);
+          for (int t = j + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NHB, PVOFF, PVS, SLO, NKQ>(t);
           return n;
         }();
         constexpr bool pv = pass_has_pv(j, NV, PVOFF, PVS);
@@ -1127,15 +1151,17 @@ void mla_partial_kernel(PartialArgs a) {
         constexpr int r = j % (PD + 1);
         // the wait ties the operands read for this step to it (a step that
         // only reuses operands needs none)
+        constexpr bool has_q = has_k && SLO + j >= NKQ;  // the Q^T operand comes from LDS too
         if constexpr (!TMLA_WAIT_PAIR) {
           if constexpr (has_k || has_v || has_p)
             lgkm_tie<after, has_k, has_v, has_p>(kb[r], vl[vi], vh[vi], pop[c][hb]);
+          if constexpr (has_q) asm volatile("" : "+v"(qb[r]));
         } else if constexpr (j % 2 == 0) {
           // one wait per two steps: the operands of steps j and j + 1
           constexpr int j2 = j + 1 < NSTEPS ? j + 1 : j;
           constexpr int after2 = [] {
             int n = 0;
-            for (int t = j2 + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NHB, PVOFF, PVS>(t);
+            for (int t = j2 + 1; t <= last; ++t) n += pass_reads<NS, NV, PV0, NHB, PVOFF, PVS, SLO, NKQ>(t);
             return n;
           }();
           constexpr bool pv1 = pass_has_pv(j2, NV, PVOFF, PVS);
@@ -1148,11 +1174,15 @@ void mla_partial_kernel(PartialArgs a) {
             tie_ops<has_k, has_v, has_p>(kb[r], vl[vi], vh[vi], pop[c][hb]);
             tie_ops<has_k1, has_v1, has_p1>(kb[j2 % (PD + 1)], vl[c1 * NDBW + j41], vh[c1 * NDBW + j41],
                                             pop[c1][hb1]);
+            if constexpr (has_q) asm volatile("" : "+v"(qb[r]));
+            if constexpr (has_k1 && SLO + j2 >= NKQ) asm volatile("" : "+v"(qb[j2 % (PD + 1)]));
           }
         }
         if constexpr (j < NS) {
           if constexpr (SLO + j == 0)
             s = mfma_vgpr_first<DT>(kb[0], qop[0]);
+          else if constexpr (has_q)
+            mfma_vgpr_acc<DT>(s, kb[r], qb[r]);
           else
             mfma_vgpr_acc<DT>(s, kb[r], qop[SLO + j]);
         }
@@ -1226,7 +1256,7 @@ void mla_partial_kernel(PartialArgs a) {
         const short* qrow = reinterpret_cast<const short*>(a.q) + (int64_t)b * a.q_sb +
                             (int64_t)(head_ok ? head : 0) * a.q_sh + 8 * hi;
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) qop[kc] = *reinterpret_cast<const i16x8*>(qrow + 16 * kc);
+        for (int kc = 0; kc < NKQ; ++kc) qop[kc] = *reinterpret_cast<const i16x8*>(qrow + 16 * kc);
       }
       asm volatile("" ::: "memory");  // the copies below are issued after Q
     };
@@ -1246,7 +1276,7 @@ void mla_partial_kernel(PartialArgs a) {
       wait_vmcnt<0>();
       if (s_owner) {
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) {
+        for (int kc = 0; kc < NKQ; ++kc) {
           const int cb = kc >> 2;
           const char LDS_AS* p = cb < NVB ? lds + qv + k_off_v[kc & 3] + cb * 1024
                                           : lds + qrope - OFF_R + k_off_v[kc & 3] + k_rope_delta + (cb - NVB) * 1024;
@@ -1532,8 +1562,10 @@ void mla_partial_kernel(PartialArgs a) {
     // initial accumulators (which would have to be kept live across the
     // first loop).
     if (b == b_first) phase_stamp(2);
+    if constexpr (F8) set_lane_offsets(lane_id_fresh());
     int i = -1;
     for (; i < 0 || i + kStages - 1 < nst; ++i) iteration(i, std::true_type{});
+    if constexpr (F8) set_lane_offsets(lane_id_fresh());
     for (; i < nst; ++i) iteration(i, std::false_type{});
     // every copy has landed and all waves are done with the rings before the
     // finalize reuses them
@@ -1588,7 +1620,9 @@ void mla_partial_kernel(PartialArgs a) {
           row_stride = DV;
         }
         // wave-uniform; only the waves that own a head block hold staged rows
-        const int rows = wave < NHB ? min(32, a.num_heads - head_base) : 0;
+        int rows = __builtin_amdgcn_readfirstlane(wave < NHB ? min(32, a.num_heads - head_base) : 0);
+        // computed per segment: 32 hoisted row conditions would crowd the SGPRs
+        asm volatile("" : "+s"(rows));
         const char LDS_AS* obuf = lds + wave * 32 * OPITCH;
         // eight rows per batch: their reads are all issued before the first
         // store waits for its data
@@ -2315,7 +2349,9 @@ void mla_partial_own_kernel(PartialArgs a) {
         dst = a.mid_o + ((int64_t)seg.slot * a.num_heads + head_base) * DV;
         row_stride = DV;
       }
-      const int rows = max(0, min(32, a.num_heads - head_base));
+      int rows = __builtin_amdgcn_readfirstlane(max(0, min(32, a.num_heads - head_base)));
+      // computed per segment: 32 hoisted row conditions would crowd the SGPRs
+      asm volatile("" : "+s"(rows));
 #pragma unroll
       for (int r0 = 0; r0 < 32; r0 += 8) {
         i16x8 row[8];
@@ -2626,13 +2662,14 @@ template <int DT>
 hipError_t launch_partial_dt(const PartialArgs& a, dim3 grid, int nhb, hipStream_t stream, bool paged, bool uni) {
   if (nhb == 1) return launch_partial_nw<DT, 1>(a, grid, stream, paged, uni);
   if (nhb == 2) return launch_partial_nw<DT, 2>(a, grid, stream, paged, uni);
-  if (TMLA_OWN_LOOP) {
+  if constexpr (TMLA_OWN_LOOP) {
     // 128 heads per workgroup: the head-owner loop
     if (!paged) return launch_partial_own_t<DT, false, false>(a, grid, stream);
     if (uni) return launch_partial_own_t<DT, true, true>(a, grid, stream);
     return launch_partial_own_t<DT, true, false>(a, grid, stream);
+  } else {
+    return launch_partial_nw<DT, 4>(a, grid, stream, paged, uni);
   }
-  return launch_partial_nw<DT, 4>(a, grid, stream, paged, uni);
 }
 
 }  // namespace tmla

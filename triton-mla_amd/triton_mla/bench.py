@@ -44,6 +44,7 @@ WORKLOADS = {
     "b32_h128_ctx8k": workloads.b32_h128_8k,
     "ragged_b64_h128_ctx1k-32k": workloads.ragged_b64_h128,
     "ragged_b64_h16_ctx1k-32k": workloads.ragged_b64_h16,
+    "b8_h64_ctx16k": workloads.b8_h64_16k,
 }
 
 

@@ -109,3 +109,8 @@ def ragged_b64_h128(dtype=torch.bfloat16):
 
 def ragged_b64_h16(dtype=torch.bfloat16):
     return ragged(64, 16, 1024, 32768, dtype, name="ragged_b64_h16_ctx1k-32k")
+
+
+def b8_h64_16k(dtype=torch.bfloat16):
+    """64 heads (one workgroup of two 32-head blocks per worker), long context."""
+    return uniform(8, 64, 16384, dtype, name="b8_h64_ctx16k")
