@@ -22,6 +22,14 @@ that no form is always the one measured first after the warm-up:
 ``value`` is the form mla_decode() runs by default; the others are reported
 beside it with min / median / p90.
 
+Then the other measured shapes (``shapes`` in the JSON line; ``--no-shapes``
+skips them and the layer): B=1 and B=8 at 1K tokens (128 heads), the ragged
+B=64 workload (1K..32K tokens, seed 0) with 128 and with 16 heads, and B=8
+with 64 heads at 16K tokens, each with its two-kernel step, partial kernel,
+HBM roofline and 70%-of-roofline target; and ``layer_step``: one decode step
+of the MLA layer at DeepSeek-V3 dims (B=16, 16K tokens), eager and replayed
+from a HIP graph, against the roofline of its weights plus cache.
+
 Then the fp8-cache legs (``fp8_cache`` and ``fp8_cache_h128`` in the JSON
 line; ``--no-fp8`` skips them): the 16-head ragged workload (B=64, 1K..32K
 tokens, page 64) and the measured 128-head workload above, each with its
@@ -68,6 +76,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on each CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-fp8", action="store_true", help="skip the fp8-cache leg (16-head ragged workload)")
+    p.add_argument("--no-shapes", action="store_true",
+                   help="skip the other decode shapes and the layer step")
     p.add_argument("--no-flush", action="store_true", help="do not evict caches between steps")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="after timing, run 3 copies of this many MiB (counter calibration)")
@@ -111,6 +121,115 @@ def cpu_baseline(inp, target_s):
     t_torch = timed(mla_decode_torch, n_torch)
     return {"cores": cores, "n_ref": n_ref, "t_ref": t_ref, "n_torch": n_torch, "t_torch": t_torch,
             "out_ref": out_ref}
+
+
+def shape_legs(args, dev, flush, stream, hosts):
+    """The decode on the other measured shapes: the two-kernel step of
+    mla_decode's default partition and its partial kernel alone, interleaved
+    rep by rep, each against the HBM roofline of its algorithmic bytes and
+    the 70% of it that the step is meant to reach (shapes whose roofline is
+    under 10 us are launch-bound: their targets are not given)."""
+    import torch
+
+    from triton_mla.kernel import DecodeLaunch
+
+    out = {}
+    for host in hosts:
+        g = host.to(dev)
+        call = DecodeLaunch(g.q, g.kv_cache, g.seqlens, g.block_table, 512, host.softmax_scale, None)
+        forms = {"step": call.run, "partial": call.partial}
+        for _ in range(max(args.warmup // 2, 2)):
+            for fn in forms.values():
+                if flush:
+                    flush()
+                fn()
+        steps = max(args.steps // 2, 10)
+        ev = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+              for k in forms}
+        torch.cuda.synchronize(dev)
+        for i in range(steps):
+            for k, fn in forms.items():
+                if flush:
+                    flush()
+                ev[k][i][0].record(stream)
+                fn()
+                ev[k][i][1].record(stream)
+        torch.cuda.synchronize(dev)
+        us = {k: [a.elapsed_time(b) * 1e3 for a, b in v] for k, v in ev.items()}
+        nbytes = host.algorithmic_bytes()
+        roof = nbytes / (HBM_PEAK_GBS * 1e9) * 1e6
+        step = statistics.median(us["step"])
+        out[host.name] = {
+            "batch": host.batch, "heads": host.heads, "tokens": int(host.seqlens.sum()),
+            "algorithmic_bytes": nbytes, "roofline_us": round(roof, 2),
+            "target_us_70pct": round(roof / 0.7, 1) if roof >= 10 else None,
+            "step_us": spread(us["step"]), "partial_us": spread(us["partial"]),
+            "step_frac": round(roof / step, 4),
+            "tflops": round(host.flops() / (step * 1e-6) / 1e12, 2),
+        }
+        del call, g
+        torch.cuda.empty_cache()
+    return out
+
+
+def layer_leg(args, dev, flush, stream):
+    """One decode step of the MLA layer at DeepSeek-V3 dims (hidden 7168,
+    q_lora 1536, latent 512 + rope 64, 128 heads), batch 16, 16384 cached
+    tokens, random weights ~ N(0, 0.02): eager (HIP glue) and replayed from
+    a HIP graph, against the HBM roofline of its weights plus cache."""
+    import torch
+
+    from triton_mla.bench import capture_layer_step
+    from triton_mla.model import MLA, MLAConfig
+
+    cfg = MLAConfig()
+    gen = torch.Generator().manual_seed(0)
+    model = MLA(cfg)
+    with torch.no_grad():
+        for name, prm in model.named_parameters():
+            if "norm" not in name:
+                prm.copy_(torch.randn(prm.shape, generator=gen) * 0.02)
+    model = model.to(dev, torch.bfloat16)
+    batch, ctx, page = 16, 16384, 64
+    pages = -(-(ctx + 1) // page)
+    cache = torch.randn(batch * pages, page, cfg.kv_cache_dim, generator=gen).to(dev, torch.bfloat16)
+    bt = torch.randperm(batch * pages, generator=gen).view(batch, pages).int().to(dev)
+    seqlens = torch.full((batch,), ctx, dtype=torch.int32, device=dev)
+    x = torch.randn(batch, cfg.hidden_size, generator=gen).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        eager = lambda: model(x, cache, seqlens, bt)  # noqa: E731
+        out_e, _ = eager()
+        graph, out_g = capture_layer_step(model, x, cache, seqlens, bt, dev)
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        same = torch.equal(out_g, out_e)
+        forms = {"eager": eager, "graph": graph.replay}
+        for _ in range(3):
+            for fn in forms.values():
+                if flush:
+                    flush()
+                fn()
+        steps = max(args.steps // 4, 10)
+        ev = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+              for k in forms}
+        torch.cuda.synchronize(dev)
+        for i in range(steps):
+            for k, fn in forms.items():
+                if flush:
+                    flush()
+                ev[k][i][0].record(stream)
+                fn()
+                ev[k][i][1].record(stream)
+        torch.cuda.synchronize(dev)
+    us = {k: [a.elapsed_time(b) * 1e3 for a, b in v] for k, v in ev.items()}
+    weight_bytes = sum(prm.numel() * prm.element_size() for prm in model.parameters())
+    kv_bytes = batch * (ctx + 1) * cfg.kv_cache_dim * 2
+    roof = (weight_bytes + kv_bytes) / (HBM_PEAK_GBS * 1e9) * 1e6
+    del graph, model, cache
+    torch.cuda.empty_cache()
+    return {"workload": "mla_layer_v3_b16_ctx16k", "weight_bytes": weight_bytes, "kv_bytes": kv_bytes,
+            "roofline_us": round(roof, 2), "step_us": spread(us["eager"]), "graph_step_us": spread(us["graph"]),
+            "graph_frac": round(roof / statistics.median(us["graph"]), 4), "graph_matches_eager": same}
 
 
 def fp8_leg(args, dev, flush, stream, host, kernel):
@@ -272,11 +391,21 @@ def main():
     except RuntimeError as exc:  # capture unsupported in this environment
         print(f"graph capture failed: {exc}", file=sys.stderr)
 
+    shapes, layer = {}, None
+    ragged16 = None
+    if not args.no_shapes:
+        ragged16 = workloads.ragged_b64_h16()
+        shapes = shape_legs(args, dev, flush, stream, [workloads.b1_h128_1k(), workloads.b8_h128_1k(),
+                                                        workloads.ragged_b64_h128(), ragged16,
+                                                        workloads.b8_h64_16k()])
+        layer = layer_leg(args, dev, flush, stream)
+
     fp8 = {}
     if not args.no_fp8:
         # 16 heads: the 16-head-group kernel; 128 heads: the 16-bit kernel
         # with the cache widened once per workgroup into its ring
-        fp8["fp8_cache"] = fp8_leg(args, dev, flush, stream, workloads.ragged_b64_h16(), "mla_partial_fp8_kernel")
+        fp8["fp8_cache"] = fp8_leg(args, dev, flush, stream, ragged16 or workloads.ragged_b64_h16(),
+                                   "mla_partial_fp8_kernel")
         fp8["fp8_cache_h128"] = fp8_leg(args, dev, flush, stream, workloads.b32_h128_8k(),
                                         "mla_partial_kernel (fp8 cache widened into the ring)")
 
@@ -333,6 +462,10 @@ def main():
         "timed_launches": {k: args.steps for k in ev},
         "graph_replay_matches_eager": graph_ok,
     }
+    if shapes:
+        result["shapes"] = shapes
+    if layer:
+        result["layer_step"] = layer
     for key, leg in fp8.items():
         result[key] = leg["summary"]
 

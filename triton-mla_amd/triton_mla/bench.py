@@ -127,7 +127,8 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
 def capture_layer_step(model, x, cache, seqlens, bt, device):
     """One MLA.forward step captured in a CUDA (HIP) graph on a side stream
     of default priority, after two eager steps there that allocate the
-    step's cached buffers; returns the graph and its output tensor."""
+    step's cached buffers (the projections' workspace of that stream, which
+    the graph then shares); returns the graph and its output tensor."""
     side = torch.cuda.Stream(device)
     side.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(side):
@@ -136,7 +137,7 @@ def capture_layer_step(model, x, cache, seqlens, bt, device):
     torch.cuda.current_stream(device).wait_stream(side)
     torch.cuda.synchronize(device)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=side):
         out, _ = model(x, cache, seqlens, bt)
     return graph, out
 
