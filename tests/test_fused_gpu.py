@@ -11,7 +11,7 @@ here the headline case is also checked against the oracle directly.
 Covered: balanced partitions with 1, 8, 16 and more than 16 workers per
 sequence; workers whose range straddles two split sequences (both of their
 merge records in use); the uniform split; empty sequences (out = 0,
-lse = -inf, cleared by the single launch itself); 16, 64, 128 and 200 heads
+lse = -inf, cleared by the single launch itself); 24, 64, 128 and 200 heads
 (one or two head blocks per worker); fp16; repeated calls on one workspace
 (the merge counters return to zero); one workspace shared by calls of
 different sizes; the hand-over path (spin limit 0: every worker that does not
@@ -69,8 +69,8 @@ def case(name):
         inp = workloads.ragged(12, 128, 0, 6000, seed=5)
         inp.seqlens[[2, 7]] = torch.tensor([0, 1], dtype=torch.int32)
         return inp
-    if name == "ragged_h16":
-        return workloads.ragged(40, 16, 0, 3000, seed=6)
+    if name == "ragged_h24":  # (16 heads or fewer run two launches: the 16-head-group kernel)
+        return workloads.ragged(40, 24, 0, 3000, seed=6)
     if name == "ragged_h64_fp16":
         return workloads.ragged(9, 64, 1, 5000, dtype=torch.float16, seed=7)
     if name == "ragged_h200":
@@ -86,7 +86,7 @@ CASES = [
     ("ragged_h128", None, None),      # up to ~90 workers per sequence, one-tile chunks
     ("ragged_h128", None, 7),         # straddling ranges
     ("ragged_h128", 4, None),         # uniform split
-    ("ragged_h16", None, 24),
+    ("ragged_h24", None, 24),
     ("ragged_h64_fp16", None, None),
     ("ragged_h64_fp16", 3, None),
     ("ragged_h200", None, 100),       # two head blocks per worker
@@ -161,7 +161,7 @@ def test_workspace_reuse_across_sizes(gpu):
 
 
 def test_workspace_reuse_across_shapes(gpu):
-    """Calls of other shapes on one workspace: a 16-head call with more
+    """Calls of other shapes on one workspace: a 24-head call with more
     sequences has a larger counter set but a smaller workspace than the
     128-head headline call that sized the buffer; its counters stay clear of
     the headline call's partials (the counter block is the same fixed size for
@@ -170,7 +170,7 @@ def test_workspace_reuse_across_shapes(gpu):
 
     lib = _native.load()
     big = launch(workloads.b32_h128_8k(), gpu)
-    wide = launch(workloads.ragged_b64_h16(), gpu)
+    wide = launch(workloads.ragged(64, 24, 1024, 32768), gpu)
     calls = {"big": big, "wide": wide}
     for name, c in calls.items():
         assert c.fused, f"{name} must take the single-launch path"

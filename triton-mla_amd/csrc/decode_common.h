@@ -304,4 +304,8 @@ __device__ __forceinline__ SegmentSlot segment_slot(const PartialArgs& a, const 
 // groups of 16); dtype is the element type of q and out.
 hipError_t launch_partial_fp8(const PartialArgs& a, dim3 grid, int dtype, bool paged, hipStream_t stream);
 
+// Stage 1 over a 16-bit cache with at most 16 heads per workgroup
+// (mla_decode_g16.hip): grid = (workers, head groups of 16).
+hipError_t launch_partial_g16(const PartialArgs& a, dim3 grid, int dtype, bool paged, hipStream_t stream);
+
 }  // namespace tmla

@@ -100,10 +100,17 @@ constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
 // fp8 cache: up to this many heads the 16-head-group kernel runs (its
 // workgroups stream the cache on their own); above, the 16-bit kernel with the
 // cache widened once per workgroup into its ring
+// 16-bit cache: up to this many heads (virtual heads of a multi-token call)
+// the 16-head-group kernel runs (mla_decode_g16.hip); 0 disables it
+#ifndef TMLA_G16_HEADS
+#define TMLA_G16_HEADS 16
+#endif
 #ifndef TMLA_FP8_GROUP_HEADS
 #define TMLA_FP8_GROUP_HEADS 16
 #endif
 constexpr int kFp8GroupHeads = TMLA_FP8_GROUP_HEADS;
+constexpr int kG16Heads = TMLA_G16_HEADS;
+static_assert(kG16Heads <= 16, "one head group per workgroup");
 
 struct CombineArgs {
   const int32_t* seqlens;
@@ -2585,6 +2592,10 @@ int worker_grid(int32_t batch, int32_t num_splits, int32_t num_workers, int64_t 
 
 // capacity_tokens: tokens the block table (or dense cache) can hold per
 // sequence; mode as in decode_launch.
+// Calls of at most kG16Heads heads (virtual heads of a multi-token call) on a
+// 16-bit cache run the 16-head-group kernel, as two launches.
+bool uses_g16(int32_t num_heads) { return num_heads <= kG16Heads; }
+
 LaunchPlan plan_launch(int32_t batch, int32_t num_heads, int32_t num_splits, int32_t num_workers,
                        int64_t capacity_tokens, size_t mid_o_bytes, int mode, int cus) {
   LaunchPlan p;
@@ -2816,6 +2827,17 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
                                      out_stride_b, out_stride_h, lse, workspace, workspace_bytes_, stream);
     return TMLA_OK;
   }
+  if (uses_g16(num_heads)) {
+    // few heads: the 16-head-group kernel (two launches, no in-kernel merge)
+    a.fused = 0;
+    const dim3 grid(worker_grid(batch, num_splits, num_workers, cap_tokens), (num_heads + 15) / 16);
+    hipError_t e = launch_partial_g16(a, grid, dtype, paged, s);
+    if (e != hipSuccess) return hip_fail(e, "mla_partial_g16_kernel launch");
+    if (mode != 0)
+      return tmla_mla_decode_combine(seqlens, batch, num_heads, head_dim_v, dtype, num_splits, num_workers, out,
+                                     out_stride_b, out_stride_h, lse, workspace, workspace_bytes_, stream);
+    return TMLA_OK;
+  }
   const LaunchPlan plan =
       plan_launch(batch, num_heads, num_splits, num_workers, cap_tokens, mid_o_bytes, mode, current_cu_count());
   const int nhb = plan.nhb;
@@ -2993,6 +3015,7 @@ int32_t tmla_mla_decode_fused_is_single(int32_t batch, int32_t num_heads, int32_
   if (batch <= 0 || num_heads <= 0 || head_dim_v != 512 || num_splits < 0 ||
       (num_splits == 0 && num_workers <= 0))
     return 0;
+  if (uses_g16(num_heads)) return 0;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
   const WsLayout wl = ws_layout(batch, num_heads, head_dim_v, num_splits, num_workers);
