@@ -1,0 +1,85 @@
+// CPU harness of the host-side planning code (triton-mla_amd/csrc/host_plan.h),
+// built by tests/test_plan_sanitize.py with the address and undefined-behaviour
+// sanitizers (any signed overflow, out-of-range shift or bad access aborts).
+// It sweeps extreme batch, head, split, worker and capacity values through
+// check_common, ws_layout, worker_grid and plan_launch and checks the
+// invariants the kernels rely on. Prints "ok <cases>" on success.
+#include <stdio.h>
+#include <stdlib.h>
+
+#include "host_plan.h"
+
+using namespace tmla;
+
+static int failures = 0;
+#define EXPECT(cond, ...)                                    \
+  do {                                                       \
+    if (!(cond)) {                                           \
+      if (failures++ < 20) {                                 \
+        fprintf(stderr, "FAIL %s: ", #cond);                 \
+        fprintf(stderr, __VA_ARGS__);                        \
+        fprintf(stderr, "\n");                               \
+      }                                                      \
+    }                                                        \
+  } while (0)
+
+int main() {
+  const int32_t I32 = INT32_MAX;
+  const int32_t batches[] = {0, 1, 7, 64, 65535, 1 << 20, I32 - 1, I32};
+  const int32_t heads[] = {1, 16, 17, 32, 33, 64, 65, 128, 129, 4096, 1 << 20, I32 - 31, I32};
+  const int32_t splits[] = {0, 1, 3, 64, 1 << 16, I32};
+  const int32_t workers[] = {0, 1, 256, 1 << 20, I32};
+  const int64_t caps[] = {0, 1, 63, 64, 8192, (int64_t)1 << 31, INT64_MAX / 2, INT64_MAX};
+  const int cus_list[] = {1, 256, 1024};
+  long cases = 0;
+  char dummy;
+  for (int32_t b : batches)
+    for (int32_t h : heads)
+      for (int32_t s : splits)
+        for (int32_t w : workers) {
+          const Common c{b, h, 512, 64, TMLA_BF16, s, w};
+          const size_t need = workspace_bytes(b, h, 512, s, w);
+          // a workspace of the size asked for is accepted; one byte less is not
+          const int rc = check_common(c, &dummy, need);
+          const bool valid_shape = b >= 0 && h > 0 && !(s == 0 && w <= 0) && !(s > 0 && (int64_t)b * s > I32);
+          if (valid_shape && need > 0) {
+            EXPECT(rc == TMLA_OK, "b=%d h=%d s=%d w=%d need=%zu rc=%d", b, h, s, w, need, rc);
+            EXPECT(check_common(c, &dummy, need - 1) == TMLA_ERR_WORKSPACE_TOO_SMALL, "b=%d h=%d", b, h);
+            const WsLayout l = ws_layout(b, h, 512, s, w);
+            const int64_t slots = partial_slots(b, s, w);
+            // partial rows and lse values fit below the counter block, 256-byte aligned
+            EXPECT(l.l >= (size_t)(slots * h) * 1024 && l.l % 256 == 0, "layout o b=%d h=%d", b, h);
+            EXPECT(l.part_end >= l.l + (size_t)(slots * h) * 4 && l.part_end % 256 == 0, "layout l b=%d h=%d", b, h);
+            EXPECT(l.total == l.part_end + kFusedCounterBytes && l.total == need, "total b=%d h=%d", b, h);
+            EXPECT((int64_t)need <= kMaxWorkspaceBytes, "bound");
+          } else if (valid_shape) {
+            // too large: rejected, never a wrapped small size
+            EXPECT(rc == TMLA_ERR_INVALID_ARGUMENT, "oversize b=%d h=%d s=%d w=%d rc=%d", b, h, s, w, rc);
+          } else {
+            EXPECT(rc != TMLA_OK, "invalid accepted b=%d h=%d s=%d w=%d", b, h, s, w);
+          }
+          if (!valid_shape) continue;
+          for (int64_t cap : caps)
+            for (int cus : cus_list)
+              for (int mode = 0; mode <= 2; ++mode) {
+                ++cases;
+                const LaunchPlan p = plan_launch(b, h, s, w, cap, need, mode, cus);
+                EXPECT(p.nhb == 1 || p.nhb == 2 || p.nhb == 4, "nhb");
+                EXPECT(p.grid_x >= 1 && p.grid_x <= I32, "grid_x %lld", (long long)p.grid_x);
+                EXPECT(p.grid_y >= 1 && p.grid_y * 32 * p.nhb >= h && (p.grid_y - 1) * 32 * p.nhb < h, "grid_y");
+                if (s > 0) EXPECT(p.grid_x == ((int64_t)b * s < 1 ? 1 : (int64_t)b * s), "uniform grid");
+                else EXPECT(p.grid_x <= w, "balanced grid within the workers");
+                if (p.fused) {
+                  EXPECT(mode == 1 && p.grid_x * p.grid_y <= cus, "fused fits the CUs");
+                  EXPECT(fused_counter_bytes(b, p.grid_y, s, w) <= (int64_t)kFusedCounterBytes, "counters fit");
+                }
+                EXPECT(head_blocks(h) >= 1, "head blocks");
+              }
+        }
+  if (failures) {
+    fprintf(stderr, "%d failures\n", failures);
+    return 1;
+  }
+  printf("ok %ld\n", cases);
+  return 0;
+}

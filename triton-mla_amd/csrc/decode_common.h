@@ -12,10 +12,10 @@
 #include <stdint.h>
 
 #include "cdna.h"
+#include "host_plan.h"
 
 namespace tmla {
 
-constexpr int kTileTokens = 64;         // planning unit (one page at page_size 64)
 constexpr float kRescaleLog2 = 8.0f;    // lazy rescale threshold (p <= 2^8)
 constexpr float kNoMax = -__FLT_MAX__;  // running max of a head that has seen no token
 constexpr float kLn2 = 0.6931471805599453f;

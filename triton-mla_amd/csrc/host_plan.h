@@ -1,0 +1,157 @@
+// Host-side planning of a decode call: argument checks, the workspace
+// layout and the launch shape. Plain C++ with no HIP dependency, so that
+// the same code is also compiled for the CPU with the address and
+// undefined-behaviour sanitizers (tests/plan_sanitize.cpp).
+//
+// All size arithmetic is done in 64 bits and checked: a call whose
+// workspace would not fit in 2^62 bytes is rejected (workspace_bytes
+// returns 0 for it), so no size can wrap around to a small value.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "triton_mla.h"
+
+namespace tmla {
+
+constexpr int kTileTokens = 64;                   // planning unit (one page at page_size 64)
+constexpr size_t kFusedCounterBytes = 256 * 1024;  // the single launch's counter block
+constexpr int64_t kMaxWorkspaceBytes = (int64_t)1 << 62;
+
+inline thread_local char g_err[512] = "no error";
+
+inline int fail(int code, const char* msg) {
+  snprintf(g_err, sizeof(g_err), "%s", msg);
+  return code;
+}
+
+// Workgroups per worker along the heads (32, 64 or 128 heads each).
+inline int64_t head_blocks(int32_t heads) {
+  const int64_t per = heads <= 32 ? 32 : heads <= 64 ? 64 : 128;
+  return ((int64_t)heads + per - 1) / per;
+}
+
+// Partial slots of a call: batch * num_splits (uniform) or num_workers +
+// batch (balanced).
+inline int64_t partial_slots(int32_t batch, int32_t splits, int32_t workers) {
+  return splits > 0 ? (int64_t)batch * splits : (int64_t)workers + batch;
+}
+
+// Workspace of a call: partial rows [slots, H, dv] (input dtype) at offset 0,
+// their base-2 lse [slots, H] (float) after them, and the fused merge's int32
+// counters m_count and m_done [batch, head blocks] and flags m_flag [slots,
+// head blocks] at the start of a block of fixed size (kFusedCounterBytes)
+// anchored at the END of the caller's buffer (its size rounded down to 256
+// bytes). Every call reserves the whole block, so no call's partials reach
+// it, whatever the shapes of the calls that share the buffer: the block is
+// zero-filled once, and every single launch leaves its counters at zero
+// again. A call whose counters exceed the block runs as two kernels.
+struct WsLayout {
+  size_t o, l, part_end;  // byte offsets: partial rows, lse, end of both
+  size_t cnt_bytes;       // counter block (a multiple of 256)
+  size_t total;           // part_end + cnt_bytes: the bytes the call needs; 0 if too large
+};
+
+inline WsLayout ws_layout(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
+  WsLayout w{0, 0, 0, kFusedCounterBytes, 0};
+  const int64_t slots = partial_slots(batch, splits, workers);
+  if (slots < 0 || heads < 0 || dv < 0) return w;
+  // rows = slots * heads, each dv * 2 bytes, all below 2^62
+  if (heads > 0 && slots > kMaxWorkspaceBytes / heads) return w;
+  const int64_t rows = slots * heads;
+  if (rows > 0 && (int64_t)dv * 2 > kMaxWorkspaceBytes / rows) return w;
+  const int64_t o_bytes = rows * dv * 2, l_bytes = rows * 4;
+  auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
+  const int64_t total = al(o_bytes) + al(l_bytes) + (int64_t)kFusedCounterBytes;
+  if (total > kMaxWorkspaceBytes) return w;
+  w.o = 0;
+  w.l = (size_t)al(o_bytes);
+  w.part_end = w.l + (size_t)al(l_bytes);
+  w.total = w.part_end + w.cnt_bytes;
+  return w;
+}
+
+// 0 for invalid or too large arguments
+inline size_t workspace_bytes(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
+  if (batch < 0 || heads <= 0 || dv < 0) return 0;
+  return ws_layout(batch, heads, dv, splits, workers).total;
+}
+
+// Bytes of the fused merge's counters and flags of a call whose grid has gy
+// workgroups along the heads.
+inline int64_t fused_counter_bytes(int32_t batch, int64_t gy, int32_t splits, int32_t workers) {
+  return (2 * (int64_t)batch + partial_slots(batch, splits, workers)) * gy * 4;
+}
+
+// Workgroups along the workers: all of them for uniform splits; for the
+// balanced partition no more than the 64-token tiles the call can hold
+// (block-table width or dense capacity: capacity_tokens per sequence), since
+// workers past them never get a range. At least 1, at most INT32_MAX.
+inline int64_t worker_grid(int32_t batch, int32_t num_splits, int32_t num_workers, int64_t capacity_tokens) {
+  if (num_splits > 0) {
+    const int64_t w = (int64_t)batch * num_splits;
+    return w < 1 ? 1 : (w > INT32_MAX ? INT32_MAX : w);
+  }
+  const int64_t cap = capacity_tokens > 0 ? capacity_tokens : 0;
+  const int64_t tiles_per_seq = cap / kTileTokens + (cap % kTileTokens != 0);
+  // batch * tiles_per_seq, saturated
+  const int64_t tile_bound =
+      batch > 0 && tiles_per_seq > INT64_MAX / batch ? INT64_MAX : (int64_t)(batch > 0 ? batch : 0) * tiles_per_seq;
+  const int64_t w = tile_bound < num_workers ? tile_bound : num_workers;
+  return w < 1 ? 1 : w;
+}
+
+// Launch shape of a decode call: blocks of 32 heads per workgroup (1, 2 or 4)
+// and the grid, and whether the single launch merges in-kernel.
+struct LaunchPlan {
+  int nhb;
+  int64_t grid_x, grid_y;
+  bool fused;
+};
+
+// capacity_tokens: tokens the block table (or dense cache) can hold per
+// sequence; mode as in decode_launch (1: the single launch if it fits);
+// cus: compute units of the device.
+inline LaunchPlan plan_launch(int32_t batch, int32_t num_heads, int32_t num_splits, int32_t num_workers,
+                              int64_t capacity_tokens, size_t mid_o_bytes, int mode, int cus) {
+  LaunchPlan p;
+  p.nhb = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
+  // When the busy workgroups would leave compute units idle, fewer heads per
+  // workgroup (more, shorter workgroups: less Q to load, less MFMA work per
+  // sub-tile, smaller partial rows) use them. (Halving keeps grid.x * grid.y
+  // within the compute units, so it never takes a call off the single launch.)
+  const int64_t heads = num_heads > 0 ? num_heads : 1;
+  p.grid_x = worker_grid(batch, num_splits, num_workers, capacity_tokens);
+  while (p.nhb > 1 && p.grid_x * ((heads + 16 * p.nhb - 1) / (16 * p.nhb)) <= cus) p.nhb /= 2;
+  const int64_t heads_per_wg = 32 * p.nhb;
+  p.grid_y = (heads + heads_per_wg - 1) / heads_per_wg;
+  // The fused merge: one workgroup per compute unit at most (the kernel's LDS
+  // use admits one), so that siblings normally run side by side; its
+  // counters (per sequence and per slot, for each workgroup along the heads)
+  // fit the workspace's counter block.
+  p.fused = mode == 1 && p.grid_x * p.grid_y <= cus && mid_o_bytes < (size_t)INT32_MAX &&
+            fused_counter_bytes(batch, p.grid_y, num_splits, num_workers) <= (int64_t)kFusedCounterBytes;
+  return p;
+}
+
+struct Common {
+  int32_t batch, heads, dv, dr, dtype, splits, workers;
+};
+
+inline int check_common(const Common& c, const void* workspace, size_t ws_bytes) {
+  if (c.batch < 0 || c.heads <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "batch must be >= 0 and num_heads > 0");
+  if (c.dtype != TMLA_BF16 && c.dtype != TMLA_FP16) return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16 or TMLA_FP16");
+  if (c.splits < 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "num_splits must be >= 0");
+  if (c.splits == 0 && c.workers <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "num_workers must be > 0 when num_splits == 0");
+  if (c.splits > 0 && (int64_t)c.batch * c.splits > INT32_MAX) return fail(TMLA_ERR_INVALID_ARGUMENT, "batch * num_splits overflows");
+  if (c.dv != 512) return fail(TMLA_ERR_UNSUPPORTED, "head_dim_v must be 512");
+  const size_t need = workspace_bytes(c.batch, c.heads, c.dv, c.splits, c.workers);
+  if (need == 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "the call's workspace would exceed 2^62 bytes");
+  if (workspace == nullptr || ws_bytes < need)
+    return fail(TMLA_ERR_WORKSPACE_TOO_SMALL, "workspace is missing or smaller than tmla_workspace_bytes()");
+  return TMLA_OK;
+}
+
+}  // namespace tmla

@@ -2495,63 +2495,9 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
 // host side
 // ---------------------------------------------------------------------------
 
-thread_local char g_err[512] = "no error";
-
-int fail(int code, const char* msg) {
-  snprintf(g_err, sizeof(g_err), "%s", msg);
-  return code;
-}
-
 int hip_fail(hipError_t e, const char* where) {
   snprintf(g_err, sizeof(g_err), "%s: %s", where, hipGetErrorString(e));
   return TMLA_ERR_HIP;
-}
-
-// Workgroups per worker along the heads (32, 64 or 128 heads each).
-int head_blocks(int32_t heads) {
-  const int per = heads <= 32 ? 32 : heads <= 64 ? 64 : 128;
-  return (heads + per - 1) / per;
-}
-
-// Workspace of a call: partial rows [slots, H, dv] (input dtype) at offset 0,
-// their base-2 lse [slots, H] (float) after them, and the fused merge's int32
-// counters m_count and m_done [batch, head blocks] and flags m_flag [slots,
-// head blocks] at the start of a block of fixed size (kFusedCounterBytes)
-// anchored at the END of the caller's buffer (its size rounded down to 256
-// bytes). Every call reserves the whole block, so no call's partials reach
-// it, whatever the shapes of the calls that share the buffer: the block is
-// zero-filled once, and every single launch leaves its counters at zero
-// again. A call whose counters exceed the block runs as two kernels.
-struct WsLayout {
-  size_t o, l, part_end;  // byte offsets: partial rows, lse, end of both
-  size_t cnt_bytes;       // counter block (a multiple of 256)
-  size_t total;           // part_end + cnt_bytes: the bytes the call needs
-};
-
-constexpr size_t kFusedCounterBytes = 256 * 1024;
-
-// Bytes of the fused merge's counters and flags of a call whose grid has gy
-// workgroups along the heads.
-int64_t fused_counter_bytes(int32_t batch, int64_t gy, int32_t splits, int32_t workers) {
-  const int64_t slots = splits > 0 ? (int64_t)batch * splits : (int64_t)workers + batch;
-  return (2 * (int64_t)batch + slots) * gy * 4;
-}
-
-WsLayout ws_layout(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
-  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  const int64_t slots = splits > 0 ? (int64_t)batch * splits : (int64_t)workers + batch;
-  WsLayout w;
-  w.o = 0;
-  w.l = al((size_t)slots * heads * dv * 2);
-  w.part_end = w.l + al((size_t)slots * heads * sizeof(float));
-  w.cnt_bytes = kFusedCounterBytes;
-  w.total = w.part_end + w.cnt_bytes;
-  return w;
-}
-
-size_t workspace_bytes(int32_t batch, int32_t heads, int32_t dv, int32_t splits, int32_t workers) {
-  if (batch < 0 || heads <= 0 || dv < 0) return 0;
-  return ws_layout(batch, heads, dv, splits, workers).total;
 }
 
 constexpr int kDefaultSpinLimit = 1 << 14;  // polls (about 2^7 clocks each) before a share is handed over
@@ -2572,54 +2518,9 @@ int current_cu_count() {
   return n;
 }
 
-// Launch shape of a decode call: blocks of 32 heads per workgroup (1, 2 or 4)
-// and the grid, and whether the single launch merges in-kernel.
-struct LaunchPlan {
-  int nhb;
-  dim3 grid;
-  bool fused;
-};
-
-// Workgroups along the workers: all of them for uniform splits; for the
-// balanced partition no more than the 64-token tiles the call can hold
-// (block-table width or dense capacity: capacity_tokens per sequence), since
-// workers past them never get a range.
-int worker_grid(int32_t batch, int32_t num_splits, int32_t num_workers, int64_t capacity_tokens) {
-  const int workers = num_splits > 0 ? batch * num_splits : num_workers;
-  const int64_t tile_bound = (int64_t)batch * ((capacity_tokens + kTileTokens - 1) / kTileTokens);
-  return num_splits > 0 ? workers : (int)(tile_bound < workers ? (tile_bound > 0 ? tile_bound : 1) : workers);
-}
-
-// capacity_tokens: tokens the block table (or dense cache) can hold per
-// sequence; mode as in decode_launch.
 // Calls of at most kG16Heads heads (virtual heads of a multi-token call) on a
 // 16-bit cache run the 16-head-group kernel, as two launches.
 bool uses_g16(int32_t num_heads) { return num_heads <= kG16Heads; }
-
-LaunchPlan plan_launch(int32_t batch, int32_t num_heads, int32_t num_splits, int32_t num_workers,
-                       int64_t capacity_tokens, size_t mid_o_bytes, int mode, int cus) {
-  LaunchPlan p;
-  p.nhb = num_heads <= 32 ? 1 : num_heads <= 64 ? 2 : 4;
-  // When the busy workgroups would leave compute units idle, fewer heads per
-  // workgroup (more, shorter workgroups: less Q to load, less MFMA work per
-  // sub-tile, smaller partial rows) use them. (Halving keeps grid.x * grid.y
-  // within the compute units, so it never takes a call off the single launch.)
-  const int grid_x = worker_grid(batch, num_splits, num_workers, capacity_tokens);
-  while (p.nhb > 1 && (int64_t)grid_x * ((num_heads + 16 * p.nhb - 1) / (16 * p.nhb)) <= cus) p.nhb /= 2;
-  const int heads_per_wg = 32 * p.nhb;
-  p.grid = dim3(grid_x, (num_heads + heads_per_wg - 1) / heads_per_wg);
-  // The fused merge: one workgroup per compute unit at most (the kernel's LDS
-  // use admits one), so that siblings normally run side by side; its
-  // counters (per sequence and per slot, for each workgroup along the heads)
-  // fit the workspace's counter block.
-  p.fused = mode == 1 && (int64_t)p.grid.x * p.grid.y <= cus && mid_o_bytes < (size_t)INT32_MAX &&
-            fused_counter_bytes(batch, p.grid.y, num_splits, num_workers) <= (int64_t)kFusedCounterBytes;
-  return p;
-}
-
-struct Common {
-  int32_t batch, heads, dv, dr, dtype, splits, workers;
-};
 
 // Scales of an fp8 cache: element strides per page (dense: per sequence)
 // and per row.
@@ -2627,19 +2528,6 @@ struct Fp8Scales {
   const float* scale;
   int64_t s0, s1;
 };
-
-int check_common(const Common& c, const void* workspace, size_t ws_bytes) {
-  if (c.batch < 0 || c.heads <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "batch must be >= 0 and num_heads > 0");
-  if (c.dtype != TMLA_BF16 && c.dtype != TMLA_FP16) return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16 or TMLA_FP16");
-  if (c.splits < 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "num_splits must be >= 0");
-  if (c.splits == 0 && c.workers <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "num_workers must be > 0 when num_splits == 0");
-  if (c.splits > 0 && (int64_t)c.batch * c.splits > INT32_MAX) return fail(TMLA_ERR_INVALID_ARGUMENT, "batch * num_splits overflows");
-  if (c.dv != 512) return fail(TMLA_ERR_UNSUPPORTED, "head_dim_v must be 512");
-  const size_t need = workspace_bytes(c.batch, c.heads, c.dv, c.splits, c.workers);
-  if (need > 0 && (workspace == nullptr || ws_bytes < need))
-    return fail(TMLA_ERR_WORKSPACE_TOO_SMALL, "workspace is missing or smaller than tmla_workspace_bytes()");
-  return TMLA_OK;
-}
 
 template <int DT, int NHB, bool PAGED, bool UNI, bool F8 = false>
 hipError_t launch_partial_t(const PartialArgs& a, dim3 grid, hipStream_t stream) {
@@ -2814,11 +2702,11 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
       const LaunchPlan plan = plan_launch(batch, num_heads, num_splits, num_workers, cap_tokens, mid_o_bytes,
                                           mode == 0 ? 0 : 2, current_cu_count());
       a.fused = 0;
-      e = dtype == TMLA_BF16 ? launch_partial_ring8<TMLA_BF16>(a, plan.grid, plan.nhb, s)
-                             : launch_partial_ring8<TMLA_FP16>(a, plan.grid, plan.nhb, s);
+      e = dtype == TMLA_BF16 ? launch_partial_ring8<TMLA_BF16>(a, dim3(plan.grid_x, plan.grid_y), plan.nhb, s)
+                             : launch_partial_ring8<TMLA_FP16>(a, dim3(plan.grid_x, plan.grid_y), plan.nhb, s);
       if (e != hipSuccess) return hip_fail(e, "mla_partial_kernel (fp8 ring) launch");
     } else {
-      const dim3 grid(worker_grid(batch, num_splits, num_workers, cap_tokens), (num_heads + 15) / 16);
+      const dim3 grid(worker_grid(batch, num_splits, num_workers, cap_tokens), ((int64_t)num_heads + 15) / 16);
       e = launch_partial_fp8(a, grid, dtype, paged, s);
     }
     if (e != hipSuccess) return hip_fail(e, "mla_partial_fp8_kernel launch");
@@ -2830,7 +2718,7 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   if (uses_g16(num_heads)) {
     // few heads: the 16-head-group kernel (two launches, no in-kernel merge)
     a.fused = 0;
-    const dim3 grid(worker_grid(batch, num_splits, num_workers, cap_tokens), (num_heads + 15) / 16);
+    const dim3 grid(worker_grid(batch, num_splits, num_workers, cap_tokens), ((int64_t)num_heads + 15) / 16);
     hipError_t e = launch_partial_g16(a, grid, dtype, paged, s);
     if (e != hipSuccess) return hip_fail(e, "mla_partial_g16_kernel launch");
     if (mode != 0)
@@ -2841,7 +2729,7 @@ int decode_launch(const void* q, int64_t q_stride_b, int64_t q_stride_h, const v
   const LaunchPlan plan =
       plan_launch(batch, num_heads, num_splits, num_workers, cap_tokens, mid_o_bytes, mode, current_cu_count());
   const int nhb = plan.nhb;
-  const dim3 grid = plan.grid;
+  const dim3 grid(plan.grid_x, plan.grid_y);
   a.mid_o_bytes = (int32_t)(mid_o_bytes < (size_t)INT32_MAX ? mid_o_bytes : 0);
   a.fused = plan.fused ? 1 : 0;
   // the single launch's counters and flags [batch | batch | slots][grid.y] at

@@ -34,6 +34,7 @@
 #include <stdio.h>
 
 #include "cdna.h"
+#include "host_plan.h"
 #include "triton_mla.h"
 
 namespace tmla {
@@ -596,7 +597,6 @@ hipError_t launch_project_dt(const ProjectArgs& a, const ProjectPlan& p, hipStre
 
 }  // namespace layer
 
-extern int fail(int code, const char* msg);
 extern int hip_fail(hipError_t e, const char* where);
 
 }  // namespace tmla
