@@ -447,7 +447,7 @@ def main():
         "config": {"workload": inp.name, "batch": inp.batch, "heads": inp.heads, "seq_len": 8192,
                    "page_size": 64, "num_splits": args.splits, "cache_flush_mib": 0 if args.no_flush else 512,
                    "form": headline},
-        "roofline": {"bound": "hbm", "kernel": "mla_partial_kernel", "achieved": round(achieved_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": "mla_partial_own_kernel", "achieved": round(achieved_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "algorithmic_bytes": nbytes,
                      "partial_us_mean": round(p_us, 2),

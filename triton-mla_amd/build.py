@@ -105,7 +105,9 @@ def build(verbose: bool = False, stamps: bool = False) -> str:
             if bad:
                 raise RuntimeError(f"{os.path.basename(asm)}: {len(bad)} reads of an inline-asm MFMA result before "
                                    f"it is ready, first: {bad[0][0]}  ->  {bad[0][1]}")
-        check_resources(usage)
+        # the profiling build's stamp code takes registers of its own: its
+        # scratch is reported, not refused
+        check_resources(usage, strict=not stamps)
         cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out + ".tmp"] + objs
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
@@ -114,7 +116,8 @@ def build(verbose: bool = False, stamps: bool = False) -> str:
     check_kernel_stubs(out + ".tmp")
     os.replace(out + ".tmp", out)
     if verbose:
-        print(f"{len(usage)} kernels, none beyond their scratch allowance, no early MFMA result reads", flush=True)
+        print(f"{len(usage)} kernels checked" + ("" if stamps else ", none beyond their scratch allowance") +
+              ", no early MFMA result reads", flush=True)
     return out
 
 
@@ -137,9 +140,9 @@ def parse_resource_usage(remarks: str) -> dict[str, dict[str, int]]:
     return usage
 
 
-def check_resources(usage: dict[str, dict[str, int]]) -> None:
+def check_resources(usage: dict[str, dict[str, int]], strict: bool = True) -> None:
     """Fail on a kernel that spills to scratch beyond its allowance or whose
-    LDS does not fit a compute unit."""
+    LDS does not fit a compute unit (strict=False: report scratch only)."""
     if not usage:
         raise RuntimeError("no kernel resource report from the compiler")
     problems = []
@@ -149,7 +152,11 @@ def check_resources(usage: dict[str, dict[str, int]]) -> None:
             continue
         allow = max([b for pat, b in SCRATCH_ALLOWANCE.items() if re.search(pat, name)], default=0)
         if u["ScratchSize"] > allow:
-            problems.append(f"{name}: {u['ScratchSize']} bytes of scratch per lane (allowed {allow})")
+            msg = f"{name}: {u['ScratchSize']} bytes of scratch per lane (allowed {allow})"
+            if strict:
+                problems.append(msg)
+            else:
+                print("note: " + msg, file=sys.stderr)
         if u.get("LDS Size", 0) > LDS_LIMIT:
             problems.append(f"{name}: {u['LDS Size']} bytes of LDS")
     if problems:
