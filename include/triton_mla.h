@@ -84,6 +84,21 @@ size_t tmla_workspace_zero_bytes(int32_t batch, int32_t num_heads, int32_t head_
                                  int32_t num_splits, int32_t num_workers);
 
 /*
+ * The balanced partition (num_splits == 0) shares the T = sum cdiv(seqlen,
+ * 64) tiles of a call among num_workers workers. With c = cdiv(T,
+ * num_workers): if the sequences cut into pieces of at most c tiles give no
+ * more than num_workers pieces, worker w takes piece w (the pieces of each
+ * sequence in order). Otherwise the tiles are laid out in order on a line on
+ * which every non-empty sequence starts with tmla_partition_segment_tiles()
+ * extra positions (the cost of a worker's start-up and finalize on a further
+ * sequence, in tiles), and worker w takes positions [w v, (w + 1) v),
+ * v = cdiv(line length, num_workers). No counterpart in the reference (its
+ * splits are uniform); for callers that predict the partition, e.g. its
+ * split counts.
+ */
+int32_t tmla_partition_segment_tiles(void);
+
+/*
  * Stage 1: split-KV partial attention.
  * Replaces the reference's `_mla_decode_stage1` launch
  * (src/triton_mla/kernel.py:276-302; kernel body kernel.py:43-138).

@@ -187,3 +187,11 @@ def test_noalloc_rejects_calls_beyond_the_scratch(lib):
     rc = lib.tmla_mla_decode_noalloc(fake, 512 * 576, 576, fake, 64 * 576, 576, 8, 64, fake, 1, 1, fake, 64, 512,
                                      512, 64, 0, 0.1, 0, 256, fake, 512 * 512, 512, fake, None)
     assert rc == 3 and b"built-in scratch" in lib.tmla_last_error()
+
+
+def test_partition_constant_matches_the_host_restatement(lib):
+    # the balanced partition's start charge, as the library reports it, is
+    # the one triton_mla.kernel.balanced_pieces assumes
+    from triton_mla.kernel import SEGMENT_START_TILES
+
+    assert lib.tmla_partition_segment_tiles() == SEGMENT_START_TILES

@@ -73,10 +73,11 @@ def test_torch_reference_functions_match_oracle():
     assert np.array_equal(bits(got), oracle.gather_kv(bits(cache), lens[:2].numpy(), bt.numpy()))
 
 
-def _partition_by_simulation(seqlens, workers):
+def _partition_by_simulation(seqlens, workers, start=2):
     """Brute force over the workers: the tiles each one takes (a snapped
-    piece, or a range of the concatenated tiles) and the sequences they
-    touch; returns the largest worker count of one sequence."""
+    piece, or a range of a line holding, per non-empty sequence, ``start``
+    positions that belong to no tile and then its tiles) and the sequences
+    they touch; returns the largest worker count of one sequence."""
     tile = 64
     tiles = [-(-n // tile) if n > 0 else 0 for n in seqlens]
     total = sum(tiles)
@@ -91,10 +92,15 @@ def _partition_by_simulation(seqlens, workers):
                 owners[b].add(w)
                 w += 1
     else:
-        seq_of_tile = [b for b, t in enumerate(tiles) for _ in range(t)]
+        line = []  # the sequence of each position, None for a start position
+        for b, t in enumerate(tiles):
+            if t:
+                line += [None] * start + [b] * t
+        v = -(-len(line) // workers)
         for w in range(workers):
-            for g in range(w * c, min((w + 1) * c, total)):
-                owners[seq_of_tile[g]].add(w)
+            for b in line[w * v:(w + 1) * v]:
+                if b is not None:
+                    owners[b].add(w)
     return max(len(o) for o in owners)
 
 
@@ -119,7 +125,8 @@ def test_balanced_pieces_matches_the_partition(seqlens, workers, expect):
     for _ in range(200):
         lens = g.integers(0, 5000, size=int(g.integers(1, 40))).tolist()
         w = int(g.integers(1, 300))
-        assert balanced_pieces(lens, w) == _partition_by_simulation(lens, w)
+        for start in (0, 2, 5):
+            assert balanced_pieces(lens, w, start) == _partition_by_simulation(lens, w, start)
 
 
 @pytest.mark.parametrize("made_in_inference", [False, True])

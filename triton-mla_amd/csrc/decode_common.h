@@ -154,11 +154,13 @@ __device__ __forceinline__ int worker_index(const PartialArgs& a) {
 
 // A worker's range: tiles [tile_lo, tile_hi) counted from the start of
 // sequence b_first (whose length is n_first; in balanced mode the range may
-// run on into the following sequences), off_first = the global tile offset
-// of b_first, chunk = tiles per worker (balanced), snapped = one piece of one
-// sequence per worker (balanced).
+// run on into the following sequences), off_first = the position of b_first's
+// first tile on the partition's line, chunk = positions per worker
+// (balanced), snapped = one piece of one sequence per worker (balanced),
+// seg_cost = positions charged for each following sequence's start
+// (straddling ranges; 0 otherwise).
 struct WorkRange {
-  int b_first, tile_lo, tile_hi, off_first, n_first, chunk;
+  int b_first, tile_lo, tile_hi, off_first, n_first, chunk, seg_cost;
   bool snapped;
 };
 
@@ -167,6 +169,7 @@ struct WorkRange {
 // only, no LDS or barrier).
 __device__ __forceinline__ bool work_range(const PartialArgs& a, int worker, WorkRange& w) {
   w.chunk = 0;
+  w.seg_cost = 0;
   w.snapped = false;
   if (a.num_splits > 0) {
     // uniform: sequence b is cut into num_splits pieces of cdiv(tiles, S)
@@ -182,21 +185,31 @@ __device__ __forceinline__ bool work_range(const PartialArgs& a, int worker, Wor
     w.off_first = 0;
     return true;
   }
-  // Balanced: the T tiles of all sequences (in order) are cut into
-  // num_workers ranges of c = cdiv(T, num_workers) tiles. Lane l sums the
-  // tile counts of sequences [l * per, (l + 1) * per), a wave-wide inclusive
-  // scan gives each lane the tile offset where its sequences end.
+  // Balanced: the T tiles of all sequences are shared by num_workers
+  // workers, c = cdiv(T, num_workers) tiles each, as one piece of one
+  // sequence per worker (snapped) or as ranges that run across sequences
+  // (straddling). Lane l sums the tile counts of sequences
+  // [l * per, (l + 1) * per), a wave-wide inclusive scan gives each lane the
+  // tile offset where its sequences end.
   const int lane0 = lane_id_fresh();
   const int per = (a.batch + 63) >> 6;
   const int lo_b = min(lane0 * per, a.batch), hi_b = min(lo_b + per, a.batch);
   const int len0 = lo_b < hi_b ? a.seqlens[lo_b] : 0;
-  int sum = tiles_of(len0);
-  for (int b = lo_b + 1; b < hi_b; ++b) sum += tiles_of(a.seqlens[b]);
+  int sum = tiles_of(len0), live = len0 > 0;
+  for (int b = lo_b + 1; b < hi_b; ++b) {
+    const int nt = tiles_of(a.seqlens[b]);
+    sum += nt;
+    live += nt > 0;
+  }
   int incl = sum;
+  int vsum = sum + kSegCostTiles * live, vincl = vsum;  // positions on the straddling line
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
-    const int v = __shfl_up(incl, d);
-    if (lane0 >= d) incl += v;
+    const int v = __shfl_up(incl, d), vv = __shfl_up(vincl, d);
+    if (lane0 >= d) {
+      incl += v;
+      vincl += vv;
+    }
   }
   const int total = __builtin_amdgcn_readlane(incl, 63);
   const int chunk = (total + a.num_workers - 1) / a.num_workers;
@@ -220,7 +233,6 @@ __device__ __forceinline__ bool work_range(const PartialArgs& a, int worker, Wor
     snapped = __builtin_amdgcn_readlane(pinc, 63) <= a.num_workers;
   }
   w.snapped = snapped;
-  const int lo = worker * chunk;
   if (snapped && worker < __builtin_amdgcn_readlane(pinc, 63)) {
     // the one lane whose sequences hold piece `worker` finds which of them
     int poff = pinc - pcs, off = incl - sum, fb = lo_b, flen = len0;
@@ -242,26 +254,40 @@ __device__ __forceinline__ bool work_range(const PartialArgs& a, int worker, Wor
     w.tile_hi = min(w.tile_lo + chunk, tiles_of(w.n_first));
     return true;
   }
-  if (snapped || lo >= total) {  // wave-uniform, and the same in every wave
+  // Straddling ranges: the sequences' tiles in order on a line where each
+  // non-empty sequence starts with kSegCostTiles extra positions (what a
+  // segment's start-up and finalize cost, in tiles), cut into num_workers
+  // ranges of vc = cdiv(VT, num_workers) positions (VT = the line's length).
+  // Tile j of sequence b sits at position voff_b + kSegCostTiles + j, so a
+  // range that holds the starts of further sequences holds fewer tiles.
+  const int vtotal = __builtin_amdgcn_readlane(vincl, 63);
+  const int vchunk = (vtotal + a.num_workers - 1) / a.num_workers;
+  const int vlo = worker * vchunk;
+  if (snapped || vlo >= vtotal) {  // wave-uniform, and the same in every wave
     w.b_first = w.off_first = w.n_first = w.tile_lo = w.tile_hi = 0;
     return false;
   }
-  // the one lane whose sequences hold tile lo finds which of them it is
-  int off = incl - sum, fb = lo_b, flen = len0;
+  w.chunk = vchunk;
+  w.seg_cost = kSegCostTiles;
+  // the one lane whose sequences hold position vlo finds which of them it is
+  int voff = vincl - vsum, fb = lo_b, flen = len0;
   for (int b = lo_b; b < hi_b; ++b) {
     const int len = b == lo_b ? len0 : a.seqlens[b];
     const int nt = tiles_of(len);
+    const int vt = nt > 0 ? nt + kSegCostTiles : 0;
     fb = b;
     flen = len;
-    if (lo < off + nt) break;
-    off += nt;
+    if (vlo < voff + vt) break;
+    voff += vt;
   }
-  const int src = __builtin_ctzll(__ballot(sum > 0 && incl - sum <= lo && lo < incl));
+  const int src = __builtin_ctzll(__ballot(vsum > 0 && vincl - vsum <= vlo && vlo < vincl));
   w.b_first = __builtin_amdgcn_readlane(fb, src);
-  w.off_first = __builtin_amdgcn_readlane(off, src);
+  w.off_first = __builtin_amdgcn_readlane(voff, src) + kSegCostTiles;  // position of b_first's tile 0
   w.n_first = __builtin_amdgcn_readlane(flen, src);
-  w.tile_lo = lo - w.off_first;                      // local to b_first
-  w.tile_hi = min(lo + chunk, total) - w.off_first;  // may run past b_first
+  // local to b_first; tile_hi may run past b_first, and is <= tile_lo when the
+  // range holds no tile at all (only positions of b_first's start)
+  w.tile_lo = max(vlo - w.off_first, 0);
+  w.tile_hi = min(vlo + vchunk, vtotal) - w.off_first;
   return true;
 }
 
@@ -287,8 +313,9 @@ __device__ __forceinline__ SegmentSlot segment_slot(const PartialArgs& a, const 
     s.first_slot = b * S;
   } else {
     const int ch = fresh_s(w.chunk);
-    // the workers of b: g1..g2 (straddling ranges) or g1 = worker - j ..
-    // g1 + pieces - 1 (snapped: this is piece j = t_start / c of b)
+    // the workers of b: g1..g2 (straddling ranges: seg_global_off = the
+    // position of b's tile 0) or g1 = worker - j .. g1 + pieces - 1
+    // (snapped: this is piece j = t_start / c of b)
     const int g1 = w.snapped ? worker - t_start / ch : seg_global_off / ch;
     const int g2 = w.snapped ? g1 + (nt_b + ch - 1) / ch - 1 : (seg_global_off + nt_b - 1) / ch;
     s.slot = worker + b;

@@ -17,6 +17,12 @@
 namespace tmla {
 
 constexpr int kTileTokens = 64;                   // planning unit (one page at page_size 64)
+// Balanced partition with straddling ranges: tiles charged for the start of
+// each sequence in a worker's range (its segment's start-up and finalize)
+#ifndef TMLA_SEG_COST_TILES
+#define TMLA_SEG_COST_TILES 2
+#endif
+constexpr int kSegCostTiles = TMLA_SEG_COST_TILES;
 constexpr size_t kFusedCounterBytes = 256 * 1024;  // the single launch's counter block
 constexpr int64_t kMaxWorkspaceBytes = (int64_t)1 << 62;
 

@@ -97,19 +97,25 @@ constexpr int kSubTokens = 32;      // LDS stage unit: M of the 32x32x16 MFMA
 #endif
 constexpr int kStages = 4;          // LDS ring depth (3 sub-tiles in flight)
 constexpr int kHeadsPerWave = 32;   // N of the 32x32x16 MFMA
-// fp8 cache: up to this many heads the 16-head-group kernel runs (its
-// workgroups stream the cache on their own); above, the 16-bit kernel with the
-// cache widened once per workgroup into its ring
 // 16-bit cache: up to this many heads (virtual heads of a multi-token call)
 // the 16-head-group kernel runs (mla_decode_g16.hip); 0 disables it
 #ifndef TMLA_G16_HEADS
 #define TMLA_G16_HEADS 16
 #endif
+// fp8 cache: up to this many heads the 16-head-group kernel runs (its
+// workgroups stream the cache on their own); above, the 16-bit kernel with the
+// cache widened once per workgroup into its ring
 #ifndef TMLA_FP8_GROUP_HEADS
 #define TMLA_FP8_GROUP_HEADS 16
 #endif
+// combine: four heads per wave when one head per wave would take more than
+// this many workgroups
+#ifndef TMLA_COMBINE_WIDE_WGS
+#define TMLA_COMBINE_WIDE_WGS 1024
+#endif
 constexpr int kFp8GroupHeads = TMLA_FP8_GROUP_HEADS;
 constexpr int kG16Heads = TMLA_G16_HEADS;
+constexpr int64_t kCombineWideWgs = TMLA_COMBINE_WIDE_WGS;
 static_assert(kG16Heads <= 16, "one head group per workgroup");
 
 struct CombineArgs {
@@ -481,11 +487,12 @@ __device__ __forceinline__ void merge_rows_at_once(const MergeView& mv, const LD
   }
 }
 
-// Any count: the max over all slots first, then eight rows in flight per batch.
-template <int DT, class LD>
+// Any count: the max over all slots first, then BATCH rows in flight per
+// batch. The result does not depend on BATCH, and equals merge_rows_at_once
+// over the same slots bit for bit (the same max, weights and order of sums).
+template <int DT, int BATCH, class LD>
 __device__ __forceinline__ void merge_row_loop(const MergeView& mv, const LD& ld, int b, int head, int slot0,
                                                int count, int lane) {
-  constexpr int BATCH = 8;
   float m = -INFINITY;
   for (int s = lane; s < count; s += 64) m = fmaxf(m, ld.lse((int64_t)(slot0 + s) * mv.num_heads + head));
   for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
@@ -564,7 +571,7 @@ __device__ __forceinline__ void merge_share(const MergeView& mv, const CoherentL
     for (int h = h_lo + 2 * wave; h < h_hi; h += 8)
       merge_rows_at_once<DT, 2, 16>(mv, ld, b, h, min(2, h_hi - h), s0, c, lane);
   } else {
-    for (int h = h_lo + wave; h < h_hi; h += 4) merge_row_loop<DT>(mv, ld, b, h, s0, c, lane);
+    for (int h = h_lo + wave; h < h_hi; h += 4) merge_row_loop<DT, 8>(mv, ld, b, h, s0, c, lane);
   }
 }
 
@@ -1668,8 +1675,8 @@ void mla_partial_kernel(PartialArgs a) {
       }
     }
 
-    remaining -= (t_end - t_start);
-    seg_global_off += nt_b;
+    remaining -= t_end - t_start + wr.seg_cost;  // the next sequence's start is charged here
+    seg_global_off += nt_b + wr.seg_cost;
     ++b;
     t_start = 0;
   }
@@ -2391,8 +2398,8 @@ void mla_partial_own_kernel(PartialArgs a) {
       }
     }
 
-    remaining -= (t_end - t_start);
-    seg_global_off += nt_b;
+    remaining -= t_end - t_start + wr.seg_cost;  // the next sequence's start is charged here
+    seg_global_off += nt_b + wr.seg_cost;
     ++b;
     t_start = 0;
   }
@@ -2407,15 +2414,21 @@ void mla_partial_own_kernel(PartialArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Stage 2: log-sum-exp merge (kernel.py:159-181). One wave per (b, head).
+// Stage 2: log-sum-exp merge (kernel.py:159-181). A workgroup merges 4 * HPW
+// heads of sequence b: one head per wave (HPW = 1), or, for calls with many
+// (sequence, head) pairs, four heads per wave (HPW = 4) so that every
+// workgroup fits the compute units in one round and each wave has four
+// heads' rows in flight. Both give the same bits.
 // ---------------------------------------------------------------------------
-template <int DT, int DV>
+template <int DT, int DV, int HPW>
 __global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
   static_assert(DV % 256 == 0, "8 dims per lane");
+  static_assert(HPW == 1 || HPW == 4, "one or four heads per wave");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b = blockIdx.x;
-  const int head = blockIdx.y * 4 + wave;
-  __shared__ int s_red[2][4];
+  const int h_lo = blockIdx.y * 4 * HPW;
+  const int h_hi = min(h_lo + 4 * HPW, a.num_heads);
+  __shared__ int s_red[3][4];
 
   // partial slots of sequence b
   const int n_b = a.seqlens[b];
@@ -2429,23 +2442,31 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
     }
     slot0 = b * S;
   } else {
-    int before = 0, total = 0;
+    // tiles in all (the snapped form), and positions before b and in all on
+    // the straddling form's line, where every non-empty sequence starts with
+    // kSegCostTiles extra positions (work_range)
+    int total = 0, vbefore = 0, vtotal = 0;
     for (int i = threadIdx.x; i < a.batch; i += 256) {
       const int nt = tiles_of(a.seqlens[i]);
+      const int vt = nt > 0 ? nt + kSegCostTiles : 0;
       total += nt;
-      if (i < b) before += nt;
+      vtotal += vt;
+      if (i < b) vbefore += vt;
     }
     for (int d = 32; d >= 1; d >>= 1) {
-      before += __shfl_xor(before, d);
       total += __shfl_xor(total, d);
+      vbefore += __shfl_xor(vbefore, d);
+      vtotal += __shfl_xor(vtotal, d);
     }
     if (lane == 0) {
-      s_red[0][wave] = before;
-      s_red[1][wave] = total;
+      s_red[0][wave] = total;
+      s_red[1][wave] = vbefore;
+      s_red[2][wave] = vtotal;
     }
     __syncthreads();
-    before = s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3];
-    total = s_red[1][0] + s_red[1][1] + s_red[1][2] + s_red[1][3];
+    total = s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3];
+    vbefore = s_red[1][0] + s_red[1][1] + s_red[1][2] + s_red[1][3];
+    vtotal = s_red[2][0] + s_red[2][1] + s_red[2][2] + s_red[2][3];
     if (nt_b > 0) {  // (then total > 0; uniform over the workgroup)
       const int chunk = (total + a.num_workers - 1) / a.num_workers;
       // the partial kernel's snapped ranges when the pieces fit the workers
@@ -2470,25 +2491,34 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(CombineArgs a) {
       if (ptotal <= a.num_workers) {
         count = (nt_b + chunk - 1) / chunk;
         slot0 = pbefore + b;
-      } else {
-        const int g1 = before / chunk, g2 = (before + nt_b - 1) / chunk;
+      } else {  // straddling: the workers whose ranges hold b's tiles
+        const int vchunk = (vtotal + a.num_workers - 1) / a.num_workers;
+        const int first = vbefore + kSegCostTiles;  // position of b's tile 0
+        const int g1 = first / vchunk, g2 = (first + nt_b - 1) / vchunk;
         count = g2 - g1 + 1;
         slot0 = g1 + b;
       }
     }
   }
-  if (head >= a.num_heads || count == 1) return;  // count == 1: written by stage 1
+  if (count == 1) return;  // written by stage 1
   static_assert(DV == 512, "one row = 64 lanes x 8 elements");
   const MergeView mv{a.mid_o, a.mid_lse, a.num_heads, a.out, a.out_sb, a.out_sh, a.lse};
   const PlainLoads ld{a.mid_o, a.mid_lse};
-  if (count == 0)
-    merge_zero(mv, b, head, lane);
-  else if (count <= 8)
-    merge_rows_at_once<DT, 1, 8>(mv, ld, b, head, 1, slot0, count, lane);
-  else if (count <= 16)
-    merge_rows_at_once<DT, 1, 16>(mv, ld, b, head, 1, slot0, count, lane);
-  else
-    merge_row_loop<DT>(mv, ld, b, head, slot0, count, lane);
+  if (count == 0) {
+    for (int h = h_lo + wave; h < h_hi; h += 4) merge_zero(mv, b, h, lane);
+  } else if (count <= 8) {
+    // HPW heads of one wave together: HPW * count rows in flight
+    const int h = h_lo + HPW * wave;
+    if (h < h_hi) merge_rows_at_once<DT, HPW, 8>(mv, ld, b, h, min(HPW, h_hi - h), slot0, count, lane);
+  } else if (count <= 16) {
+    constexpr int P = HPW == 4 ? 2 : 1;  // heads per pass
+    for (int h = h_lo + P * wave; h < h_hi; h += 4 * P)
+      merge_rows_at_once<DT, P, 16>(mv, ld, b, h, min(P, h_hi - h), slot0, count, lane);
+  } else if (count <= 32) {  // e.g. a few long sequences cut over all workers: one round trip
+    for (int h = h_lo + wave; h < h_hi; h += 4) merge_rows_at_once<DT, 1, 32>(mv, ld, b, h, 1, slot0, count, lane);
+  } else {
+    for (int h = h_lo + wave; h < h_hi; h += 4) merge_row_loop<DT, 32>(mv, ld, b, h, slot0, count, lane);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2585,6 +2615,8 @@ size_t tmla_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v
                             int32_t num_workers) {
   return workspace_bytes(batch, num_heads, head_dim_v, num_splits, num_workers);
 }
+
+int32_t tmla_partition_segment_tiles(void) { return kSegCostTiles; }
 
 int tmla_debug_stamps(void* host, size_t bytes) {
 #if TMLA_STAMPS
@@ -2832,12 +2864,22 @@ int tmla_mla_decode_combine(const int32_t* seqlens, int32_t batch, int32_t num_h
   const WsLayout wl = ws_layout(batch, num_heads, 512, num_splits, num_workers);
   a.mid_o = reinterpret_cast<const short*>(ws + wl.o);
   a.mid_lse = reinterpret_cast<const float*>(ws + wl.l);
-  dim3 grid(batch, (num_heads + 3) / 4);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == TMLA_BF16)
-    hipLaunchKernelGGL((mla_combine_kernel<TMLA_BF16, 512>), grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((mla_combine_kernel<TMLA_FP16, 512>), grid, dim3(256), 0, s, a);
+  // four heads per wave once one head per wave would take more than
+  // kCombineWideWgs workgroups
+  const bool wide = (int64_t)batch * ((num_heads + 3) / 4) > kCombineWideWgs;
+  const dim3 grid(batch, wide ? (num_heads + 15) / 16 : (num_heads + 3) / 4);
+  if (dtype == TMLA_BF16) {
+    if (wide)
+      hipLaunchKernelGGL((mla_combine_kernel<TMLA_BF16, 512, 4>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((mla_combine_kernel<TMLA_BF16, 512, 1>), grid, dim3(256), 0, s, a);
+  } else {
+    if (wide)
+      hipLaunchKernelGGL((mla_combine_kernel<TMLA_FP16, 512, 4>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((mla_combine_kernel<TMLA_FP16, 512, 1>), grid, dim3(256), 0, s, a);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "mla_combine_kernel launch");
   return TMLA_OK;

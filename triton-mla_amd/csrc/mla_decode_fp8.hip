@@ -474,8 +474,8 @@ void mla_partial_fp8_kernel(PartialArgs a) {
       __syncthreads();  // the staging is read before the next segment's copies land
     }
 
-    remaining -= t_end - t_start;
-    seg_global_off += nt_b;
+    remaining -= t_end - t_start + wr.seg_cost;  // the next sequence's start is charged here
+    seg_global_off += nt_b + wr.seg_cost;
     ++b;
     t_start = 0;
   }

@@ -29,6 +29,7 @@ SIGNATURES = {
     "tmla_device_cu_count": (_i32, [_i32]),
     "tmla_debug_stamps": (ctypes.c_int, [_vp, _sz]),
     "tmla_workspace_zero_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "tmla_partition_segment_tiles": (_i32, []),
     "tmla_mla_decode_fused_is_single": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64, _i32]),
     "tmla_mla_decode_partial": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,

@@ -68,17 +68,25 @@ def get_num_splits(batch, num_heads, max_seqlen, num_sms, min_tokens_per_split=1
     return 1 << (splits.bit_length() - 1)
 
 
-def balanced_pieces(seqlens, num_workers: int) -> int:
+# Positions the balanced partition's straddling ranges charge for the start
+# of each non-empty sequence (csrc/host_plan.h kSegCostTiles; the library
+# reports its value through tmla_partition_segment_tiles).
+SEGMENT_START_TILES = 2
+
+
+def balanced_pieces(seqlens, num_workers: int, segment_tiles: int = SEGMENT_START_TILES) -> int:
     """Largest number of workers the balanced partition (``num_splits=None``)
     gives one sequence of ``seqlens`` (host integers), i.e. its split count.
 
     Host restatement of the device planner (csrc/decode_common.h work_range /
-    segment_slot): the T = sum cdiv(n, 64) tiles are cut into ranges of
-    c = cdiv(T, num_workers) tiles; when the sequences cut into pieces of at
-    most c tiles make no more pieces than workers, each sequence has
-    cdiv(tiles, c) pieces ("snapped"), otherwise a sequence at global tile
-    offset o is covered by the workers o // c .. (o + tiles - 1) // c.
-    0 when every sequence is empty.
+    segment_slot): with T = sum cdiv(n, 64) tiles and c = cdiv(T,
+    num_workers), when the sequences cut into pieces of at most c tiles make
+    no more pieces than workers, each sequence has cdiv(tiles, c) pieces
+    ("snapped"). Otherwise the tiles lie in order on a line where each
+    non-empty sequence starts with ``segment_tiles`` extra positions, cut into
+    ranges of v = cdiv(line length, num_workers) positions: a sequence whose
+    first tile is at position p is covered by the workers
+    p // v .. (p + tiles - 1) // v. 0 when every sequence is empty.
     """
     tiles = [_cdiv(int(n), 64) if int(n) > 0 else 0 for n in seqlens]
     total = sum(tiles)
@@ -87,11 +95,14 @@ def balanced_pieces(seqlens, num_workers: int) -> int:
     c = _cdiv(total, num_workers)
     if sum(_cdiv(t, c) for t in tiles) <= num_workers:
         return max(_cdiv(t, c) for t in tiles)
+    line = [t + segment_tiles if t else 0 for t in tiles]
+    v = _cdiv(sum(line), num_workers)
     best, off = 0, 0
-    for t in tiles:
+    for t, span in zip(tiles, line):
         if t:
-            best = max(best, (off + t - 1) // c - off // c + 1)
-        off += t
+            p = off + segment_tiles
+            best = max(best, (p + t - 1) // v - p // v + 1)
+        off += span
     return best
 
 
