@@ -376,6 +376,26 @@ int tmla_mla_rms_norm(const void* x, int64_t x_stride, const void* weight, float
                       int32_t dim, int32_t dtype, void* y, int64_t y_stride, void* stream);
 
 /*
+ * The query latent's RMSNorm (tmla_mla_rms_norm on batch rows of q_dim) and
+ * the cache append of the new token (tmla_mla_kv_append) in one launch, with
+ * the same arithmetic and bits as the two calls, plus next_positions[b] =
+ * positions[b] + 1 (the sequence lengths after the step, which the step's
+ * decode reads). The two read different rows of the step's first projection
+ * and do not depend on each other. Replaces `q_norm` (src/triton_mla/
+ * model.py:76), the kv half of `MLA._project` and `MLA._append_kv`
+ * (model.py:80-94) and `cache_seqlens + 1` (model.py:109) of one step.
+ */
+int tmla_mla_norm_append(const void* q_lat, int64_t q_lat_stride, const void* q_norm_weight,
+                         float q_eps, int32_t q_dim, void* q_out, int64_t q_out_stride,
+                         const void* kv_proj, int64_t kv_proj_stride_b, const void* kv_norm_weight,
+                         float kv_eps, float rope_theta, const int32_t* positions,
+                         int32_t* next_positions, int32_t batch, int32_t kv_lora_rank,
+                         int32_t rope_dim, int32_t dtype, void* kv_cache, int64_t kv_stride_0,
+                         int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
+                         const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols,
+                         void* stream);
+
+/*
  * Dense projection of a decode step's rows: y[m, n] = x[m, :] . w[n, :]
  * (float32 accumulation, rounded once to the dtype), i.e. nn.Linear without
  * bias with w in its [out_features, in_features] layout. Replaces the

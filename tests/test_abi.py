@@ -141,6 +141,25 @@ def test_layer_glue_arguments_rejected_on_host(lib):
     assert lib.tmla_mla_kv_append(*args) == 1 and b"page_size" in lib.tmla_last_error()
     args = list(k); args[13] = 0
     assert lib.tmla_mla_kv_append(*args) == 1
+    # tmla_mla_norm_append(q_lat, q_s, q_w, q_eps, q_dim, q_out, qo_s, kv_proj, sb, kv_w, kv_eps, theta,
+    #                      positions, next_positions, batch, rank, rope, dtype, cache, s0, s1, num_blocks,
+    #                      page_size, bt, bt_sb, bt_cols, stream)
+    na = [fake, 1536, fake, 1e-6, 1536, fake, 1536, fake, 576, None, 1e-6, 1e4, fake, fake, 2, 512, 64, 0,
+          fake, 64 * 576, 576, 4, 64, fake, 4, 4, None]
+    args = list(na); args[4] = 1540; args[1] = 1544; args[6] = 1544
+    assert lib.tmla_mla_norm_append(*args) == 2  # q_dim not a multiple of 8
+    args = list(na); args[16] = 32
+    assert lib.tmla_mla_norm_append(*args) == 2  # rope_dim other than 64
+    args = list(na); args[13] = None
+    assert lib.tmla_mla_norm_append(*args) == 1 and b"null" in lib.tmla_last_error()
+    args = list(na); args[5] = None
+    assert lib.tmla_mla_norm_append(*args) == 1 and b"null" in lib.tmla_last_error()
+    args = list(na); args[23] = None  # dense cache needs page_size 1
+    assert lib.tmla_mla_norm_append(*args) == 1 and b"page_size" in lib.tmla_last_error()
+    args = list(na); args[17] = 3
+    assert lib.tmla_mla_norm_append(*args) == 1 and b"dtype" in lib.tmla_last_error()
+    args = list(na); args[14] = 0
+    assert lib.tmla_mla_norm_append(*args) == 0  # empty batch: nothing to do
     # tmla_mla_rms_norm(x, x_s, w, eps, rows, dim, dtype, y, y_s, stream)
     rn = [fake, 1536, fake, 1e-6, 16, 1536, 0, fake, 1536, None]
     args = list(rn); args[5] = 1540; args[1] = 1544; args[8] = 1544

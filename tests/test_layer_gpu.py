@@ -163,6 +163,44 @@ def test_absorb_out_matches_oracle(gpu, batch, heads):
     assert_matches(bits(out.cpu()), ref, dot_bound(rank, abs_sum), f"o . W_UV (B={batch}, H={heads})")
 
 
+@pytest.mark.parametrize("layout", ["paged64", "dense"])
+@pytest.mark.parametrize("batch", [1, 7, 16])
+def test_norm_append_equals_the_two_calls(gpu, layout, batch):
+    """tmla_mla_norm_append (the query latent's RMSNorm and the cache append in
+    one launch) gives the bits of tmla_mla_rms_norm and tmla_mla_kv_append
+    run separately, leaves the same cache, and returns positions + 1 (a
+    position past the block table included: its row is not written, its
+    length still advances)."""
+    from triton_mla import layer_ops
+
+    gen = torch.Generator().manual_seed(batch * 7 + len(layout))
+    rank, rope, qd = 512, 64, 1536
+    positions = torch.randint(0, 500, (batch,), generator=gen, dtype=torch.int32)
+    positions[-1] = 511 if layout == "dense" else 512  # paged: one past the table's last row
+    q_lat = (2.0 * torch.randn(batch, qd, generator=gen)).to(torch.bfloat16)
+    q_w = (1.0 + 0.3 * torch.randn(qd, generator=gen)).to(torch.bfloat16)
+    kv_proj = torch.randn(batch, rank + rope, generator=gen).to(torch.bfloat16)
+    kv_w = (1.0 + 0.3 * torch.randn(rank, generator=gen)).to(torch.bfloat16)
+    if layout == "dense":
+        cache = torch.randn(batch, 512, rank + rope, generator=gen).to(torch.bfloat16)
+        bt = None
+    else:
+        cache = torch.randn(batch * 8, 64, rank + rope, generator=gen).to(torch.bfloat16)
+        bt = torch.randperm(batch * 8, generator=gen).view(batch, 8).int().to(gpu)
+    c1, c2 = cache.to(gpu), cache.to(gpu)
+    pos = positions.to(gpu)
+    y1 = layer_ops.rms_norm(q_lat.to(gpu), q_w.to(gpu), 1e-6)
+    layer_ops.kv_append(kv_proj.to(gpu), kv_w.to(gpu), 1e-6, ROPE_THETA, pos, c1, bt, rank, rope)
+    y2, nxt = layer_ops.norm_append(q_lat.to(gpu), q_w.to(gpu), 1e-6, kv_proj.to(gpu), kv_w.to(gpu), 1e-6,
+                                    ROPE_THETA, pos, c2, bt, rank, rope)
+    torch.cuda.synchronize(gpu)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert torch.equal(c1.view(torch.int16), c2.view(torch.int16))
+    assert nxt.dtype == torch.int32 and torch.equal(nxt.cpu(), positions + 1)
+    if batch > 1 or layout == "dense":  # (batch 1 paged: the only position lies past the table)
+        assert not torch.equal(c2.cpu().view(torch.int16), cache.view(torch.int16))  # rows were appended
+
+
 @pytest.mark.parametrize("rows,dim,strided", [(16, 1536, True), (3, 512, False), (9, 4104, False)])
 def test_rms_norm_matches_oracle(gpu, rows, dim, strided):
     """RMSNorm of rows (tmla_mla_rms_norm) against the float64 oracle's

@@ -75,6 +75,7 @@ struct KvAppendArgs {
   const short* norm_w;   // [rank] or null
   float eps, theta;
   const int32_t* pos;    // [B]
+  int32_t* pos_next;     // [B] or null: pos + 1 (the sequence lengths after the step)
   char* cache;           // paged [num_blocks, page_size, rank+rope] or dense [B, capacity, rank+rope]
   int64_t s0, s1;        // byte strides
   int64_t num_blocks;    // pages (paged) or capacity (dense)
@@ -277,11 +278,9 @@ __global__ __launch_bounds__(256) void mla_absorb_out_kernel(AbsorbOutArgs a) {
 // cache append: one wave per sequence, grid cdiv(batch, 4)
 // ---------------------------------------------------------------------------
 template <int DT>
-__global__ __launch_bounds__(256) void mla_kv_append_kernel(KvAppendArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (b >= a.batch) return;
+__device__ __forceinline__ void kv_append_row(const KvAppendArgs& a, int b, int lane) {
   const int pos = a.pos[b];
+  if (a.pos_next && lane == 0) a.pos_next[b] = pos + 1;
   // destination row; rows outside the table or the cache are not written
   char* dst = nullptr;
   if (pos >= 0) {
@@ -325,6 +324,12 @@ __global__ __launch_bounds__(256) void mla_kv_append_kernel(KvAppendArgs a) {
   }
 }
 
+template <int DT>
+__global__ __launch_bounds__(256) void mla_kv_append_kernel(KvAppendArgs a) {
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b < a.batch) kv_append_row<DT>(a, b, threadIdx.x & 63);  // wave-uniform
+}
+
 // ---------------------------------------------------------------------------
 // RMSNorm of rows (the query latent): grid (cdiv(rows, 4)), one wave per row
 // ---------------------------------------------------------------------------
@@ -343,10 +348,7 @@ struct RmsNormArgs {
 // 8-element chunks l, l + 64, ...; the row is read twice (the second pass
 // from cache).
 template <int DT>
-__global__ __launch_bounds__(256) void mla_rms_norm_kernel(RmsNormArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= a.rows) return;  // wave-uniform
+__device__ __forceinline__ void rms_norm_row(const RmsNormArgs& a, int row, int lane) {
   const short* x = a.x + (int64_t)row * a.x_s;
   const int chunks = a.dim / 8;
   float ss = 0.0f;
@@ -374,6 +376,29 @@ __global__ __launch_bounds__(256) void mla_rms_norm_kernel(RmsNormArgs a) {
       o[e] = Elt<DT>::from_float(f);
     }
     *reinterpret_cast<i16x8*>(y + 8 * j) = o;
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void mla_rms_norm_kernel(RmsNormArgs a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row < a.rows) rms_norm_row<DT>(a, row, threadIdx.x & 63);  // wave-uniform
+}
+
+// The query latent's RMSNorm and the cache append of one step in one launch
+// (they read different rows of the same GEMM output and do not depend on each
+// other): workgroups [0, cdiv(rows, 4)) normalise query rows, the rest append
+// one sequence per wave, with the same per-row code as the two kernels above.
+template <int DT>
+__global__ __launch_bounds__(256) void mla_norm_append_kernel(RmsNormArgs r, KvAppendArgs k) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nq = (r.rows + 3) / 4;
+  if ((int)blockIdx.x < nq) {
+    const int row = blockIdx.x * 4 + wave;
+    if (row < r.rows) rms_norm_row<DT>(r, row, lane);
+  } else {
+    const int b = (blockIdx.x - nq) * 4 + wave;
+    if (b < k.batch) kv_append_row<DT>(k, b, lane);
   }
 }
 
@@ -681,11 +706,18 @@ int tmla_mla_absorb_out(const void* o_latent, int64_t o_stride_b, int64_t o_stri
   return e == hipSuccess ? TMLA_OK : hip_fail(e, "mla_absorb_out_kernel launch");
 }
 
-int tmla_mla_kv_append(const void* kv_proj, int64_t kv_proj_stride_b, const void* norm_weight, float eps,
-                       float rope_theta, const int32_t* positions, int32_t batch, int32_t kv_lora_rank,
-                       int32_t rope_dim, int32_t dtype, void* kv_cache, int64_t kv_stride_0, int64_t kv_stride_1,
-                       int64_t num_blocks, int32_t page_size, const int32_t* block_table, int64_t bt_stride_b,
-                       int32_t bt_cols, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Checks the arguments of a cache append and fills its kernel arguments;
+// TMLA_OK with batch 0 means nothing to do.
+int kv_append_args(const void* kv_proj, int64_t kv_proj_stride_b, const void* norm_weight, float eps,
+                   float rope_theta, const int32_t* positions, int32_t batch, int32_t kv_lora_rank, int32_t rope_dim,
+                   int32_t dtype, void* kv_cache, int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks,
+                   int32_t page_size, const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols,
+                   KvAppendArgs& a) {
+  a = KvAppendArgs{};
   if (batch < 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "batch must be >= 0");
   if (dtype != TMLA_BF16 && dtype != TMLA_FP16) return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16 or TMLA_FP16");
   if (rope_dim != kRope || kv_lora_rank <= 0 || kv_lora_rank % 64 != 0 || kv_lora_rank > 1024)
@@ -695,7 +727,6 @@ int tmla_mla_kv_append(const void* kv_proj, int64_t kv_proj_stride_b, const void
   if (num_blocks <= 0 || page_size <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "num_blocks and page_size must be > 0");
   if (block_table && bt_cols <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "block_table needs at least one column");
   if (!block_table && page_size != 1) return fail(TMLA_ERR_INVALID_ARGUMENT, "dense cache requires page_size == 1");
-  KvAppendArgs a{};
   a.kvp = static_cast<const short*>(kv_proj);
   a.kvp_sb = kv_proj_stride_b;
   a.norm_w = static_cast<const short*>(norm_weight);
@@ -712,6 +743,48 @@ int tmla_mla_kv_append(const void* kv_proj, int64_t kv_proj_stride_b, const void
   a.bt_cols = bt_cols;
   a.batch = batch;
   a.rank = kv_lora_rank;
+  return TMLA_OK;
+}
+
+// Checks the arguments of a row RMSNorm and fills its kernel arguments; TMLA_OK
+// with rows 0 means nothing to do.
+int rms_norm_args(const void* x, int64_t x_stride, const void* weight, float eps, int32_t rows, int32_t dim,
+                  int32_t dtype, void* y, int64_t y_stride, RmsNormArgs& a) {
+  a = RmsNormArgs{};
+  if (rows < 0 || dim <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "rows must be >= 0 and dim > 0");
+  if (dtype != TMLA_BF16 && dtype != TMLA_FP16) return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16 or TMLA_FP16");
+  if (dim % 8 != 0) return fail(TMLA_ERR_UNSUPPORTED, "rms_norm is built for dim a multiple of 8");
+  if (rows == 0) return TMLA_OK;
+  if (!x || !y) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)weight) & 15)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "x, weight and y must be 16-byte aligned");
+  if ((x_stride | y_stride) & 7 || x_stride < dim || y_stride < dim)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "row strides must be multiples of 8 elements and >= dim");
+  a.x = static_cast<const short*>(x);
+  a.x_s = x_stride;
+  a.w = static_cast<const short*>(weight);
+  a.y = static_cast<short*>(y);
+  a.y_s = y_stride;
+  a.eps = eps;
+  a.rows = rows;
+  a.dim = dim;
+  return TMLA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tmla_mla_kv_append(const void* kv_proj, int64_t kv_proj_stride_b, const void* norm_weight, float eps,
+                       float rope_theta, const int32_t* positions, int32_t batch, int32_t kv_lora_rank,
+                       int32_t rope_dim, int32_t dtype, void* kv_cache, int64_t kv_stride_0, int64_t kv_stride_1,
+                       int64_t num_blocks, int32_t page_size, const int32_t* block_table, int64_t bt_stride_b,
+                       int32_t bt_cols, void* stream) {
+  KvAppendArgs a;
+  const int rc = kv_append_args(kv_proj, kv_proj_stride_b, norm_weight, eps, rope_theta, positions, batch,
+                                kv_lora_rank, rope_dim, dtype, kv_cache, kv_stride_0, kv_stride_1, num_blocks,
+                                page_size, block_table, bt_stride_b, bt_cols, a);
+  if (rc != TMLA_OK || batch == 0) return rc;
   dim3 grid((batch + 3) / 4);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TMLA_BF16)
@@ -724,24 +797,9 @@ int tmla_mla_kv_append(const void* kv_proj, int64_t kv_proj_stride_b, const void
 
 int tmla_mla_rms_norm(const void* x, int64_t x_stride, const void* weight, float eps, int32_t rows, int32_t dim,
                       int32_t dtype, void* y, int64_t y_stride, void* stream) {
-  if (rows < 0 || dim <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "rows must be >= 0 and dim > 0");
-  if (dtype != TMLA_BF16 && dtype != TMLA_FP16) return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16 or TMLA_FP16");
-  if (dim % 8 != 0) return fail(TMLA_ERR_UNSUPPORTED, "rms_norm is built for dim a multiple of 8");
-  if (rows == 0) return TMLA_OK;
-  if (!x || !y) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
-  if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)weight) & 15)
-    return fail(TMLA_ERR_INVALID_ARGUMENT, "x, weight and y must be 16-byte aligned");
-  if ((x_stride | y_stride) & 7 || x_stride < dim || y_stride < dim)
-    return fail(TMLA_ERR_INVALID_ARGUMENT, "row strides must be multiples of 8 elements and >= dim");
-  RmsNormArgs a{};
-  a.x = static_cast<const short*>(x);
-  a.x_s = x_stride;
-  a.w = static_cast<const short*>(weight);
-  a.y = static_cast<short*>(y);
-  a.y_s = y_stride;
-  a.eps = eps;
-  a.rows = rows;
-  a.dim = dim;
+  RmsNormArgs a;
+  const int rc = rms_norm_args(x, x_stride, weight, eps, rows, dim, dtype, y, y_stride, a);
+  if (rc != TMLA_OK || rows == 0) return rc;
   dim3 grid((rows + 3) / 4);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TMLA_BF16)
@@ -750,6 +808,33 @@ int tmla_mla_rms_norm(const void* x, int64_t x_stride, const void* weight, float
     hipLaunchKernelGGL(mla_rms_norm_kernel<TMLA_FP16>, grid, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? TMLA_OK : hip_fail(e, "mla_rms_norm_kernel launch");
+}
+
+int tmla_mla_norm_append(const void* q_lat, int64_t q_lat_stride, const void* q_norm_weight, float q_eps,
+                         int32_t q_dim, void* q_out, int64_t q_out_stride, const void* kv_proj,
+                         int64_t kv_proj_stride_b, const void* kv_norm_weight, float kv_eps, float rope_theta,
+                         const int32_t* positions, int32_t* next_positions, int32_t batch, int32_t kv_lora_rank,
+                         int32_t rope_dim, int32_t dtype, void* kv_cache, int64_t kv_stride_0, int64_t kv_stride_1,
+                         int64_t num_blocks, int32_t page_size, const int32_t* block_table, int64_t bt_stride_b,
+                         int32_t bt_cols, void* stream) {
+  RmsNormArgs r;
+  KvAppendArgs k;
+  int rc = rms_norm_args(q_lat, q_lat_stride, q_norm_weight, q_eps, batch, q_dim, dtype, q_out, q_out_stride, r);
+  if (rc != TMLA_OK) return rc;
+  rc = kv_append_args(kv_proj, kv_proj_stride_b, kv_norm_weight, kv_eps, rope_theta, positions, batch, kv_lora_rank,
+                      rope_dim, dtype, kv_cache, kv_stride_0, kv_stride_1, num_blocks, page_size, block_table,
+                      bt_stride_b, bt_cols, k);
+  if (rc != TMLA_OK || batch == 0) return rc;
+  if (!next_positions) return fail(TMLA_ERR_INVALID_ARGUMENT, "null pointer argument");
+  k.pos_next = next_positions;
+  dim3 grid(2 * ((batch + 3) / 4));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TMLA_BF16)
+    hipLaunchKernelGGL(mla_norm_append_kernel<TMLA_BF16>, grid, dim3(256), 0, s, r, k);
+  else
+    hipLaunchKernelGGL(mla_norm_append_kernel<TMLA_FP16>, grid, dim3(256), 0, s, r, k);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TMLA_OK : hip_fail(e, "mla_norm_append_kernel launch");
 }
 
 size_t tmla_mla_project_workspace_bytes(int32_t m, int32_t n, int32_t k) {

@@ -30,6 +30,9 @@ SIGNATURES = {
     "tmla_debug_stamps": (ctypes.c_int, [_vp, _sz]),
     "tmla_workspace_zero_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "tmla_partition_segment_tiles": (_i32, []),
+    "tmla_mla_norm_append": (ctypes.c_int, [
+        _vp, _i64, _vp, _f32, _i32, _vp, _i64, _vp, _i64, _vp, _f32, _f32, _vp, _vp, _i32, _i32, _i32, _i32, _vp,
+        _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp]),
     "tmla_mla_decode_fused_is_single": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64, _i32]),
     "tmla_mla_decode_partial": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32,

@@ -113,6 +113,49 @@ PROJECT_PAYS_ROWS = 16
 PROJECT_PAYS_COLUMNS = 4096
 
 
+def norm_append(q_lat, q_norm_weight, q_eps, kv_proj, kv_norm_weight, kv_eps, rope_theta, positions, kv_cache,
+                block_table, kv_lora_rank, rope_dim):
+    """rms_norm(q_lat) and kv_append(kv_proj, ...) of one step in one launch
+    (tmla_mla_norm_append, the same bits as the two calls). Returns the
+    normalised query latent and positions + 1 (int32, the sequence lengths
+    after the step)."""
+    dev = _check_gpu(q_lat, kv_proj, kv_cache)
+    assert q_lat.dim() == 2 and q_lat.stride(1) == 1 and q_lat.dtype == kv_proj.dtype
+    assert kv_proj.dtype == kv_cache.dtype and kv_proj.stride(-1) == 1 and kv_cache.stride(-1) == 1
+    if kv_cache.dim() == 4:  # FlashMLA layout [..., 1, D]
+        kv_cache = kv_cache.squeeze(2)
+    batch, q_dim = q_lat.shape
+    assert kv_proj.shape[0] == batch
+    assert kv_proj.shape[1] == kv_lora_rank + rope_dim and kv_cache.shape[-1] == kv_lora_rank + rope_dim
+    positions = positions.to(device=dev, dtype=torch.int32).contiguous()
+    if q_norm_weight is not None:
+        q_norm_weight = q_norm_weight.to(device=dev, dtype=q_lat.dtype).contiguous()
+    if kv_norm_weight is not None:
+        kv_norm_weight = kv_norm_weight.to(kv_proj.dtype).contiguous()
+    if block_table is not None:
+        block_table = block_table.to(device=dev, dtype=torch.int32)
+        if block_table.stride(-1) != 1:
+            block_table = block_table.contiguous()
+        bt = (block_table.data_ptr(), block_table.stride(0), block_table.shape[1])
+        num_blocks, page_size = kv_cache.shape[0], kv_cache.shape[1]
+    else:
+        assert kv_cache.shape[0] == batch
+        bt = (None, 0, 1)
+        num_blocks, page_size = kv_cache.shape[1], 1
+    q_out = torch.empty(batch, q_dim, dtype=q_lat.dtype, device=dev)
+    next_positions = torch.empty(batch, dtype=torch.int32, device=dev)
+    lib = _native.load()
+    with torch.cuda.device(dev):
+        _native.check(lib.tmla_mla_norm_append(
+            q_lat.data_ptr(), q_lat.stride(0), None if q_norm_weight is None else q_norm_weight.data_ptr(),
+            float(q_eps), q_dim, q_out.data_ptr(), q_out.stride(0),
+            kv_proj.data_ptr(), kv_proj.stride(0), None if kv_norm_weight is None else kv_norm_weight.data_ptr(),
+            float(kv_eps), float(rope_theta), positions.data_ptr(), next_positions.data_ptr(), batch, kv_lora_rank,
+            rope_dim, _native.DTYPE_CODE[kv_proj.dtype], kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1),
+            num_blocks, page_size, *bt, _stream(dev)), "tmla_mla_norm_append")
+    return q_out, next_positions
+
+
 def rms_norm(x, weight, eps):
     """RMSNorm of the rows of a 2-D x (model.py:34-41): float32, the
     normalised value times the weight rounded once (tmla_mla_rms_norm)."""

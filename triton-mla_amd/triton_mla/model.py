@@ -152,12 +152,14 @@ class MLA(nn.Module):
             # take the reference's torch glue, which casts (model.py:108-124)
             return self.forward_torch_glue(x, kv_cache, cache_seqlens, block_table, num_splits)
         q_lat, kv_proj = self._down_proj(x)  # [B, q_lora_rank], [B, rank + rope]
-        q_lat = layer_ops.rms_norm(q_lat, self.q_norm.weight, self.q_norm.eps)
+        # in one launch: q_norm (model.py:76); RMSNorm(c_kv), RoPE(k_pe) and
+        # the paged append (model.py:80-94); cache_seqlens + 1 (model.py:109)
+        q_lat, seqlens = layer_ops.norm_append(
+            q_lat, self.q_norm.weight, self.q_norm.eps, kv_proj, self.kv_norm.weight, self.kv_norm.eps,
+            cfg.rope_theta, cache_seqlens, kv_cache, block_table, cfg.kv_lora_rank, cfg.qk_rope_head_dim)
+        if seqlens.dtype != cache_seqlens.dtype:  # the caller's dtype, as cache_seqlens + 1 keeps it
+            seqlens = seqlens.to(cache_seqlens.dtype)
         q_proj = self._linear(self.wq_b, q_lat)  # [B, H * (nope + rope)]
-        # RMSNorm(c_kv), RoPE(k_pe) and the paged append (model.py:80-94)
-        layer_ops.kv_append(kv_proj, self.kv_norm.weight, self.kv_norm.eps, cfg.rope_theta, cache_seqlens,
-                            kv_cache, block_table, cfg.kv_lora_rank, cfg.qk_rope_head_dim)
-        seqlens = cache_seqlens + 1
         # q = [q_nope . W_UK, RoPE(q_pe)] (model.py:74-79, 108-109)
         q = layer_ops.absorb_q(q_proj, self.wkv_b.weight, cache_seqlens, cfg.num_heads, cfg.qk_nope_head_dim,
                                cfg.qk_rope_head_dim, cfg.kv_lora_rank, cfg.v_head_dim, cfg.rope_theta)
