@@ -163,8 +163,9 @@ int tmla_mla_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
 /*
  * The same call as ONE launch (no counterpart in the reference, which always
  * launches two kernels): when every workgroup of stage 1 fits on the device
- * at once (workers times head blocks of up to 128 heads at most the CU
- * count; tmla_mla_decode_fused_is_single tells), the workers of a split
+ * at once (workers times head blocks at most the CU count: blocks of up to
+ * 128 heads, of 16 heads for calls of at most 16 heads;
+ * tmla_mla_decode_fused_is_single tells), the workers of a split
  * sequence merge its partials themselves, each a share of the heads, once
  * all of them have stored theirs (a bounded wait of spin_limit polls, about
  * 2^7 clocks apart; < 0 selects the default, 16384; 0 makes every worker

@@ -2,7 +2,7 @@
 // built by tests/test_plan_sanitize.py with the address and undefined-behaviour
 // sanitizers (any signed overflow, out-of-range shift or bad access aborts).
 // It sweeps extreme batch, head, split, worker and capacity values through
-// check_common, ws_layout, worker_grid and plan_launch and checks the
+// check_common, ws_layout, worker_grid, plan_launch and plan_launch_g16 and checks the
 // invariants the kernels rely on. Prints "ok <cases>" on success.
 #include <stdio.h>
 #include <stdlib.h>
@@ -74,6 +74,14 @@ int main() {
                   EXPECT(fused_counter_bytes(b, p.grid_y, s, w) <= (int64_t)kFusedCounterBytes, "counters fit");
                 }
                 EXPECT(head_blocks(h) >= 1, "head blocks");
+                // the 16-head-group kernel's plan: 16 heads per workgroup
+                const LaunchPlan g = plan_launch_g16(b, h, s, w, cap, need, mode, cus);
+                EXPECT(g.grid_x == p.grid_x, "g16 grid_x");
+                EXPECT(g.grid_y >= 1 && g.grid_y * 16 >= h && (g.grid_y - 1) * 16 < h, "g16 grid_y");
+                if (g.fused) {
+                  EXPECT(mode == 1 && g.grid_x * g.grid_y <= cus, "g16 fused fits the CUs");
+                  EXPECT(fused_counter_bytes(b, g.grid_y, s, w) <= (int64_t)kFusedCounterBytes, "g16 counters fit");
+                }
               }
         }
   if (failures) {

@@ -80,9 +80,9 @@ def test_workspace_zero_suffix(lib):
     # a smaller call's counters fit inside a larger call's suffix
     assert lib.tmla_workspace_zero_bytes(8, 128, 512, 0, 256) <= lib.tmla_workspace_zero_bytes(32, 128, 512, 0, 256)
     assert lib.tmla_mla_decode_fused_is_single(0, 128, 512, 0, 256, 8192, 0) == 0  # empty batch: nothing fuses
-    # 16 heads or fewer run the 16-head-group kernel: always two launches
-    assert lib.tmla_mla_decode_fused_is_single(4, 16, 512, 0, 256, 8192, 0) == 0
-    assert lib.tmla_mla_decode_fused_is_single(4, 1, 512, 2, 0, 8192, 0) == 0
+    # invalid arguments never fuse
+    assert lib.tmla_mla_decode_fused_is_single(4, 16, 512, -1, 256, 8192, 0) == 0
+    assert lib.tmla_mla_decode_fused_is_single(4, 1, 256, 2, 0, 8192, 0) == 0
 
 
 def _partial(lib, **kw):

@@ -11,8 +11,9 @@ here the headline case is also checked against the oracle directly.
 Covered: balanced partitions with 1, 8, 16 and more than 16 workers per
 sequence; workers whose range straddles two split sequences (both of their
 merge records in use); the uniform split; empty sequences (out = 0,
-lse = -inf, cleared by the single launch itself); 24, 64, 128 and 200 heads
-(one or two head blocks per worker); fp16; repeated calls on one workspace
+lse = -inf, cleared by the single launch itself); 3, 16, 24, 64, 128 and 200
+heads (the 16-head-group kernel up to 16 heads; one or two head blocks per
+worker above); fp16; repeated calls on one workspace
 (the merge counters return to zero); one workspace shared by calls of
 different sizes; the hand-over path (spin limit 0: every worker that does not
 complete the count gives its share to the one that does); and HIP-graph
@@ -69,8 +70,16 @@ def case(name):
         inp = workloads.ragged(12, 128, 0, 6000, seed=5)
         inp.seqlens[[2, 7]] = torch.tensor([0, 1], dtype=torch.int32)
         return inp
-    if name == "ragged_h24":  # (16 heads or fewer run two launches: the 16-head-group kernel)
+    if name == "ragged_h24":
         return workloads.ragged(40, 24, 0, 3000, seed=6)
+    if name == "ragged_h16":  # the 16-head-group kernel; empty and 1-token sequences
+        inp = workloads.ragged(40, 16, 0, 3000, seed=9)
+        inp.seqlens[[3, 11]] = torch.tensor([0, 1], dtype=torch.int32)
+        return inp
+    if name == "ragged_h3":  # one partly used 16-head group
+        inp = workloads.ragged(20, 3, 0, 5000, seed=10)
+        inp.seqlens[5] = 0
+        return inp
     if name == "ragged_h64_fp16":
         return workloads.ragged(9, 64, 1, 5000, dtype=torch.float16, seed=7)
     if name == "ragged_h200":
@@ -87,6 +96,10 @@ CASES = [
     ("ragged_h128", None, 7),         # straddling ranges
     ("ragged_h128", 4, None),         # uniform split
     ("ragged_h24", None, 24),
+    ("ragged_h16", None, None),
+    ("ragged_h16", None, 24),         # straddling ranges
+    ("ragged_h16", 4, None),          # uniform split
+    ("ragged_h3", None, None),
     ("ragged_h64_fp16", None, None),
     ("ragged_h64_fp16", 3, None),
     ("ragged_h200", None, 100),       # two head blocks per worker
@@ -110,7 +123,7 @@ def test_single_launch_equals_two_kernels(gpu, name, splits, workers):
         assert torch.all(out[empty.to(gpu)] == 0) and torch.all(torch.isneginf(lse[empty.to(gpu)]))
 
 
-@pytest.mark.parametrize("name,splits,workers", [CASES[0], CASES[2], CASES[3], CASES[5]])
+@pytest.mark.parametrize("name,splits,workers", [CASES[0], CASES[2], CASES[3], CASES[5], CASES[6], CASES[7]])
 def test_hand_over_path(gpu, name, splits, workers):
     """Spin limit 0 (a per-call argument): a worker that does not complete
     its sequence's count hands its share over at once; the worker that

@@ -142,6 +142,20 @@ inline LaunchPlan plan_launch(int32_t batch, int32_t num_heads, int32_t num_spli
   return p;
 }
 
+// Launch shape of a call that runs the 16-head-group kernel (workgroups of
+// 16 heads along grid.y); the single launch under the conditions of
+// plan_launch.
+inline LaunchPlan plan_launch_g16(int32_t batch, int32_t num_heads, int32_t num_splits, int32_t num_workers,
+                                  int64_t capacity_tokens, size_t mid_o_bytes, int mode, int cus) {
+  LaunchPlan p;
+  p.nhb = 0;
+  p.grid_x = worker_grid(batch, num_splits, num_workers, capacity_tokens);
+  p.grid_y = ((int64_t)(num_heads > 0 ? num_heads : 1) + 15) / 16;
+  p.fused = mode == 1 && p.grid_x * p.grid_y <= cus && mid_o_bytes < (size_t)INT32_MAX &&
+            fused_counter_bytes(batch, p.grid_y, num_splits, num_workers) <= (int64_t)kFusedCounterBytes;
+  return p;
+}
+
 struct Common {
   int32_t batch, heads, dv, dr, dtype, splits, workers;
 };

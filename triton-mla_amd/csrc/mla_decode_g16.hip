@@ -41,6 +41,7 @@
 #include "cdna.h"
 #include "decode_common.h"
 #include "group16.h"
+#include "merge.h"
 #include "triton_mla.h"
 
 namespace tmla {
@@ -130,10 +131,26 @@ void mla_partial_g16_kernel(PartialArgs a) {
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // slice of each tile
   const int worker = worker_index(a);
-  WorkRange wr;
-  if (!work_range(a, worker, wr) || wr.tile_lo >= wr.tile_hi) return;
   const int head0 = blockIdx.y * kHeads;
   const int nh = min(kHeads, a.num_heads - head0);
+  // single launch: this workgroup's merge records (first and last segment:
+  // b, its index among b's workers, their count, b's first slot, whether its
+  // arrival completed the count) and the tail's messages
+  __shared__ int s_pend[2][5];
+  __shared__ int s_msg[4];
+  WorkRange wr;
+  const bool has_range = work_range(a, worker, wr) && wr.tile_lo < wr.tile_hi;
+  if (a.fused) {
+    if (threadIdx.x == 0) s_pend[0][0] = s_pend[1][0] = -1;
+    // empty sequences worker, worker + nwg, ...: out = 0, lse = -inf
+    // (kernel.py:126-128, 178-181); the combine kernel does this otherwise
+    const MergeView mv{a.mid_o, a.mid_lse, a.num_heads, a.out, a.out_sb, a.out_sh, a.lse};
+    const int lane = lane_id_fresh();
+    for (int bb = worker; bb < a.batch; bb += gridDim.x)
+      if (tiles_of(a.seqlens[bb]) == 0)
+        for (int h = head0 + wave; h < head0 + nh; h += 4) merge_zero(mv, bb, h, lane);
+  }
+  if (!has_range) return;  // (a workgroup without a range has no merge records)
   char LDS_AS* const ring = lds + wave * kRing;
 
   int b = wr.b_first;
@@ -149,6 +166,13 @@ void mla_partial_g16_kernel(PartialArgs a) {
     }
     const int t_end = min(nt_b, t_start + remaining);
     const SegmentSlot ss = segment_slot(a, wr, worker, b, t_start, nt_b, seg_global_off);
+    if (a.fused && !ss.direct && threadIdx.x == 0) {
+      int* rec = s_pend[b == wr.b_first ? 0 : 1];
+      rec[0] = b;
+      rec[1] = ss.index;
+      rec[2] = ss.count;
+      rec[3] = ss.first_slot;
+    }
 
     const int lane = lane_id_fresh();
     const int g = lane >> 4, r = lane & 15;
@@ -389,11 +413,30 @@ void mla_partial_g16_kernel(PartialArgs a) {
       }
       __syncthreads();  // the staging is read before the next segment's copies land
     }
+    if (a.fused && !ss.direct) {
+      // every wave's write-through partial row and lse stores have completed
+      // before the arrival
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const int old = sys_add(a.m_count + (int64_t)b * gridDim.y + blockIdx.y, 1);
+        int* rec = s_pend[b == wr.b_first ? 0 : 1];
+        rec[4] = old == rec[2] - 1;  // this arrival completed the count
+      }
+    }
 
     remaining -= t_end - t_start + wr.seg_cost;  // the next sequence's start is charged here
     seg_global_off += nt_b + wr.seg_cost;
     ++b;
     t_start = 0;
+  }
+
+  if (a.fused) {
+    const CoherentLoads ld{
+        __builtin_amdgcn_make_buffer_rsrc(a.mid_o, 0, a.mid_o_bytes, kBufferWord3),
+        __builtin_amdgcn_make_buffer_rsrc(a.mid_lse, 0, a.mid_o_bytes / 256, kBufferWord3)};
+    fused_merge_tail<DT>(MergeView{a.mid_o, a.mid_lse, a.num_heads, a.out, a.out_sb, a.out_sh, a.lse}, ld,
+                         a.m_count, a.m_done, a.m_flag, a.spin_limit, wave, s_pend, s_msg, kHeads);
   }
 }
 
