@@ -25,18 +25,21 @@ SCALE = 192 ** -0.5
 WIDE_WGS = 1024
 
 
-def _inputs(batch, heads, max_len, seed):
+def _inputs(batch, heads, max_len, seed, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     seqlens = torch.randint(0, max_len + 1, (batch,), generator=g, dtype=torch.int32)
     seqlens[:4] = torch.tensor([0, 1, max_len, 64 * 33 + 5], dtype=torch.int32)
-    q = torch.randn(batch, heads, D, generator=g).to(torch.bfloat16)
-    kv = torch.randn(batch, max_len, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(batch, heads, D, generator=g).to(dtype)
+    kv = torch.randn(batch, max_len, D, generator=g).to(dtype)
     return q, kv, seqlens
 
 
-@pytest.mark.parametrize("heads", [20, 40])
-@pytest.mark.parametrize("splits", [4, 12, 24, 40])
-def test_wide_combine_matches_narrow(gpu, heads, splits):
+@pytest.mark.parametrize("heads,splits,dtype", [(20, 4, torch.bfloat16), (20, 12, torch.bfloat16),
+                                                (20, 24, torch.bfloat16), (20, 40, torch.bfloat16),
+                                                (40, 4, torch.bfloat16), (40, 12, torch.bfloat16),
+                                                (40, 24, torch.bfloat16), (40, 40, torch.bfloat16),
+                                                (40, 12, torch.float16)])
+def test_wide_combine_matches_narrow(gpu, heads, splits, dtype):
     import triton_mla
 
     max_len = 64 * 48
@@ -44,7 +47,8 @@ def test_wide_combine_matches_narrow(gpu, heads, splits):
     assert big * -(-heads // 4) > WIDE_WGS
     small = 12
     assert small * -(-heads // 4) <= WIDE_WGS
-    q, kv, seqlens = _inputs(big, heads, max_len, seed=heads * 100 + splits)
+    dname = "fp16" if dtype == torch.float16 else "bf16"
+    q, kv, seqlens = _inputs(big, heads, max_len, seed=heads * 100 + splits, dtype=dtype)
     qd, kvd, sd = q.to(gpu), kv.to(gpu), seqlens.to(gpu)
     out_big, lse_big = triton_mla.mla_decode(qd, kvd, sd, None, 512, SCALE, num_splits=splits, return_lse=True)
     out_small, lse_small = triton_mla.mla_decode(qd[:small].contiguous(), kvd[:small].contiguous(), sd[:small], None,
@@ -54,7 +58,7 @@ def test_wide_combine_matches_narrow(gpu, heads, splits):
     assert torch.equal(lse_big[:small], lse_small)
 
     ref_out, ref_lse = oracle.mla_decode_ref(bits(q[:small]), bits(kv[:small]), seqlens[:small].numpy(), None, 512,
-                                             SCALE, dtype="bf16")
+                                             SCALE, dtype=dname)
     torch.testing.assert_close(out_small.float().cpu(), torch.from_numpy(ref_out), atol=1e-2, rtol=1e-2)
     valid = seqlens[:small] > 0
     torch.testing.assert_close(lse_small.cpu()[valid], torch.from_numpy(ref_lse)[valid], atol=1e-3, rtol=1e-3)
@@ -63,6 +67,6 @@ def test_wide_combine_matches_narrow(gpu, heads, splits):
     # empty and one-token sequences included)
     pick = np.r_[0:4, big - 3:big]
     ref_out, ref_lse = oracle.mla_decode_ref(bits(q[pick]), bits(kv[pick]), seqlens[pick].numpy(), None, 512, SCALE,
-                                             dtype="bf16")
+                                             dtype=dname)
     torch.testing.assert_close(out_big[pick].float().cpu(), torch.from_numpy(ref_out), atol=1e-2, rtol=1e-2)
     assert torch.all(out_big[0] == 0) and torch.all(torch.isneginf(lse_big[0]))
