@@ -209,10 +209,13 @@ __global__ __launch_bounds__(256) void mla_absorb_q_kernel(AbsorbQArgs a) {
     }
   }
 
-  // RoPE of q_pe: the first column block of every batch tile; rows x pairs
-  // over the 256 threads
-  if (blockIdx.y == 0) {
-    for (int idx = threadIdx.x; idx < kBTile * (kRope / 2); idx += 256) {
+  // RoPE of q_pe: rows x pairs of the batch tile, shared by the workgroups
+  // of all column blocks (each rotation costs a power and a large-argument
+  // sine and cosine: kept in one column block, they made its workgroups the
+  // last to finish)
+  {
+    const int nthreads = 256 * gridDim.y;
+    for (int idx = threadIdx.x + 256 * blockIdx.y; idx < kBTile * (kRope / 2); idx += nthreads) {
       const int b = b0 + idx / (kRope / 2), i = idx % (kRope / 2);
       if (b >= a.batch) break;
       const short* pe = a.qp + (int64_t)b * a.qp_sb + (int64_t)h * (kNope + kRope) + kNope;
