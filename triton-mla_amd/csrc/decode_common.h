@@ -69,15 +69,15 @@ __device__ __forceinline__ int tiles_of(int n) { return n > 0 ? (n + kTileTokens
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
+// Keeps an int in a VGPR at this point (vector address arithmetic instead of
+// one scalar register pair per use).
+__device__ __forceinline__ void pin_i1(int& a) { asm volatile("" : "+v"(a)); }
+
 // The lane id through an instruction the compiler cannot look through:
 // offsets derived from it are recomputed where they are needed instead of
 // being kept live across the whole kernel (where they would be spilled to
 // scratch and reloaded, one memory round trip each, at start-up and in the
 // finalize).
-// Keeps an int in a VGPR at this point (vector address arithmetic instead of
-// one scalar register pair per use).
-__device__ __forceinline__ void pin_i1(int& a) { asm volatile("" : "+v"(a)); }
-
 __device__ __forceinline__ int lane_id_fresh() {
   int v;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(v));
