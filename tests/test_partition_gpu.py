@@ -94,3 +94,35 @@ def test_head_blocks_for_small_batches(gpu, batch):
     for o, l in ((out, lse), (out1, lse1)):
         torch.testing.assert_close(o.float().cpu(), torch.from_numpy(ref_out), **OUT_TOL)
         torch.testing.assert_close(l.cpu(), torch.from_numpy(ref_lse), **LSE_TOL)
+
+
+@pytest.mark.parametrize("heads", [16, 64, 128])
+def test_ranges_across_many_sequences(gpu, heads):
+    """120 short sequences over 16 workers: each straddling range holds about
+    eight sequence starts (the walk charges each of them on the partition's
+    line), most of its segments are whole sequences written directly, and
+    its first and last ones are shared with the neighbouring workers. Both
+    forms against the oracle, and the single launch equal to the two kernels."""
+    from triton_mla.kernel import DecodeLaunch
+
+    g = torch.Generator().manual_seed(heads)
+    lens = torch.randint(0, 400, (120,), generator=g, dtype=torch.int32)
+    lens[[5, 17, 18]] = torch.tensor([0, 1, 64], dtype=torch.int32)
+    seqlens = lens.tolist()
+    workers = 16
+    assert pieces(seqlens, workers) > workers  # the straddling form
+    batch, per_seq = len(seqlens), -(-max(seqlens) // TILE)
+    q = torch.randn(batch, heads, D_LATENT + D_ROPE, generator=g).to(torch.bfloat16)
+    kv = torch.randn(batch * per_seq, TILE, D_LATENT + D_ROPE, generator=g).to(torch.bfloat16)
+    bt = torch.randperm(batch * per_seq, generator=g).view(batch, per_seq).int()
+    call = DecodeLaunch(q.to(gpu), kv.to(gpu), lens.to(gpu), bt.to(gpu), D_LATENT, SCALE, None, workers)
+    out, lse = call.run()
+    out, lse = out.clone(), lse.clone()
+    out1, lse1 = call.run(single_launch=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out1) and torch.equal(lse, lse1)
+    ref_out, ref_lse = oracle.mla_decode_ref(bits(q), bits(kv), lens.numpy(), bt.numpy(), D_LATENT, SCALE)
+    valid = lens > 0
+    torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref_out), **OUT_TOL)
+    torch.testing.assert_close(lse.cpu()[valid], torch.from_numpy(ref_lse)[valid], **LSE_TOL)
+    assert torch.all(out.cpu()[~valid] == 0) and torch.all(torch.isneginf(lse.cpu()[~valid]))
