@@ -38,10 +38,42 @@ from triton_mla.timing import Flusher  # noqa: E402
 WORKERS, SLOTS = 4096, 9
 
 
+def print_spread(run, wg, rt, ck, t0):
+    """Percentiles over the workgroups of one launch, then per-XCD medians."""
+    cols = dict(
+        entry_us=(rt[:, 0] - t0) / 100,
+        loop_start_us=(rt[:, 2] - t0) / 100,
+        loop_end_us=(rt[:, 3] - t0) / 100,
+        end_us=(rt[:, 4] - t0) / 100,
+        loop_us=(rt[:, 3] - rt[:, 2]) / 100,
+        ghz=(ck[:, 3] - ck[:, 2]) / np.maximum(1, (rt[:, 3] - rt[:, 2]) * 10.0),
+    )
+    print(f"run {run}: {len(wg)} workgroups", flush=True)
+    for k, v in cols.items():
+        q = np.percentile(v, [0, 10, 50, 90, 100])
+        print(f"  {k:14s} min {q[0]:8.2f}  p10 {q[1]:8.2f}  p50 {q[2]:8.2f}  p90 {q[3]:8.2f}  max {q[4]:8.2f}")
+    xcd = wg % 8
+    line = "  per XCD (median loop_us / end_us / ghz):"
+    for x in range(8):
+        m = xcd == x
+        if m.any():
+            line += (f" {x}: {np.median(cols['loop_us'][m]):.1f}/{np.median(cols['end_us'][m]):.1f}"
+                     f"/{np.median(cols['ghz'][m]):.2f}")
+    print(line, flush=True)
+    late = np.argsort(cols["end_us"])[-4:]
+    print("  latest workgroups (id: entry, loop start, loop end, end us):",
+          "; ".join(f"{wg[i]}: {cols['entry_us'][i]:.1f}, {cols['loop_start_us'][i]:.1f}, "
+                    f"{cols['loop_end_us'][i]:.1f}, {cols['end_us'][i]:.1f}" for i in late), flush=True)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--reps", type=int, default=25)
     p.add_argument("--workload", default="b32_h128_ctx8k", choices=sorted(WORKLOADS))
+    p.add_argument("--spread", action="store_true",
+                   help="also print, per run, percentiles over workgroups of entry, loop end and end "
+                        "(from the first entry), loop time and clocks per sub-tile, and the medians of "
+                        "the workgroups of each XCD (workgroup x runs on XCD x mod 8)")
     args = p.parse_args()
     dev = torch.device("cuda:0")
     inp = WORKLOADS[args.workload]().to(dev)
@@ -62,8 +94,11 @@ def main():
         s = buf[: nwg * SLOTS * 2].reshape(nwg, SLOTS, 2).astype(np.int64)
         rt, ck = s[:, :, 0], s[:, :, 1]
         ok = (rt[:, 4] > rt[:, 0]) & (rt[:, 0] > 0)  # workgroups with a segment
+        wg = np.nonzero(ok)[0]
         rt, ck = rt[ok], ck[ok]
         t0 = rt[:, 0].min()
+        if args.spread and it < 6:
+            print_spread(it, wg, rt, ck, t0)
         nsub = float(np.median((ck[:, 3] - ck[:, 2]))) / max(1.0, float(np.median(ck[:, 8] - ck[:, 5])))
         it_ok = (rt[:, 8] > rt[:, 5])
         r = dict(
