@@ -8,7 +8,8 @@
  * that stream; no entry point synchronises the host or allocates memory.
  * Every entry point returns a tmla_status (0 = success).
  *
- * Element codes (`dtype`): TMLA_BF16, TMLA_FP16. q, kv and out share it.
+ * Element codes (`dtype`): TMLA_BF16, TMLA_FP16 (every decode entry point),
+ * TMLA_FP32 (tmla_mla_decode_generic only). q, kv and out share it.
  *
  * Work partition. Stage 1 runs a grid of workers; each worker owns a
  * contiguous range of 64-token KV tiles and, for every sequence that range
@@ -41,7 +42,7 @@ typedef enum {
     TMLA_ERR_HIP = 4
 } tmla_status;
 
-enum { TMLA_BF16 = 0, TMLA_FP16 = 1 };
+enum { TMLA_BF16 = 0, TMLA_FP16 = 1, TMLA_FP32 = 2 };
 
 /* Human-readable text for a status returned by the last failing call on this
  * thread (includes the HIP error string for TMLA_ERR_HIP). */
@@ -289,6 +290,35 @@ int tmla_mla_decode_fp8_partial(const void* q, int64_t q_stride_b, int64_t q_str
                                 float softmax_scale, int32_t num_splits, int32_t num_workers, void* out,
                                 int64_t out_stride_b, int64_t out_stride_h, float* lse, void* workspace,
                                 size_t workspace_bytes, void* stream);
+/*
+ * Decode for the head dims and element types the kernels above are not built
+ * for. The reference's kernels take any power-of-two head_dim_v and rope_dim
+ * (src/triton_mla/kernel.py:243-244) and any element type shared by q and
+ * the cache (kernel.py:245); this entry point takes head_dim_v a power of
+ * two in [16, 1024], rope_dim a power of two in [16, 256] and dtype
+ * TMLA_BF16, TMLA_FP16 or TMLA_FP32, and runs both of the reference's
+ * stages the reference's way: sequence b is cut into num_splits pieces of
+ * cdiv(seqlens[b], num_splits) tokens (kernel.py:84-86), one workgroup per
+ * (16 heads, piece, sequence), each writing a float32 partial and its base-2
+ * log-sum-exp (kernel.py:43-138, launch kernel.py:276-302), which a second
+ * kernel merges (kernel.py:141-181, launch kernel.py:303-320). Scores and
+ * sums in float32, probabilities rounded to dtype for the value product
+ * (kernel.py:123). Vector ALU arithmetic (no matrix cores): for unusual
+ * dims, not for speed. Arguments mean what they mean for tmla_mla_decode;
+ * num_splits in [1, 65535]; batch and num_heads at most 65535; the
+ * workspace is tmla_generic_workspace_bytes(batch, num_heads, head_dim_v,
+ * num_splits) bytes and needs no initialisation. Sequence lengths above the
+ * cache's capacity are cut to it.
+ */
+size_t tmla_generic_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v, int32_t num_splits);
+int tmla_mla_decode_generic(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
+                            int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
+                            const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols,
+                            const int32_t* seqlens, int32_t batch, int32_t num_heads, int32_t head_dim_v,
+                            int32_t rope_dim, int32_t dtype, float softmax_scale, int32_t num_splits, void* out,
+                            int64_t out_stride_b, int64_t out_stride_h, float* lse, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /*
  * Profiling hook, no counterpart in the reference: copies the partial
  * kernel's phase stamps of the last launch into `host` (up to `bytes`):

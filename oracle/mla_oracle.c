@@ -42,7 +42,11 @@
  *                      per-token scales, and per-page == per-token scales
  *                      that repeat the page's value.
  *
- * Element types: 0 = bfloat16, 1 = float16 (raw 16-bit patterns).
+ * Element types: 0 = bfloat16, 1 = float16 (raw 16-bit patterns), 2 =
+ * float32 (mla_decode_ref only: q and the cache as float arrays; the
+ * reference's kernels take any element type q and the cache share,
+ * kernel.py:245). Pinned like the 16-bit types, and equal to them bit for
+ * bit on values both can hold.
  */
 #include <math.h>
 #include <stdint.h>
@@ -54,6 +58,7 @@
 
 #define ORACLE_BF16 0
 #define ORACLE_FP16 1
+#define ORACLE_FP32 2
 
 /* Exact widening of a 16-bit float pattern. */
 static double half_bits_to_double(uint16_t h, int dtype) {
@@ -143,7 +148,13 @@ void oracle_gather_kv(const uint16_t* kv, int64_t kv_s0, int64_t kv_s1, const in
  * (reference.py:16-31). Writes out (float32, unrounded) and the natural-log
  * lse of the heads of b. Returns 2 on an allocation failure.
  */
-static int attend_rows(const double* k, int64_t n, const uint16_t* q, int64_t q_sb, int64_t q_sh, int64_t b,
+/* Element i of a q or cache array of element type dtype, exactly. */
+static double elem_to_double(const void* base, int64_t i, int dtype) {
+    if (dtype == ORACLE_FP32) return (double)((const float*)base)[i];
+    return half_bits_to_double(((const uint16_t*)base)[i], dtype);
+}
+
+static int attend_rows(const double* k, int64_t n, const void* q, int64_t q_sb, int64_t q_sh, int64_t b,
                        int64_t heads, int64_t dqk, int64_t dv, int dtype, double scale, float* out, float* lse) {
     int failed = 0;
 #pragma omp parallel
@@ -157,8 +168,7 @@ static int attend_rows(const double* k, int64_t n, const uint16_t* q, int64_t q_
         } else {
 #pragma omp for schedule(dynamic, 1)
             for (int64_t h = 0; h < heads; ++h) {
-                const uint16_t* qr = q + b * q_sb + h * q_sh;
-                for (int64_t c = 0; c < dqk; ++c) qd[c] = half_bits_to_double(qr[c], dtype);
+                for (int64_t c = 0; c < dqk; ++c) qd[c] = elem_to_double(q, b * q_sb + h * q_sh + c, dtype);
                 double m = -INFINITY;
                 for (int64_t t = 0; t < n; ++t) {
                     const double* kr = k + t * dqk;
@@ -201,7 +211,7 @@ static void empty_sequence(int64_t b, int64_t heads, int64_t dv, float* out, flo
  * [B, H, dv] (not rounded: the caller rounds to the input dtype), lse is
  * float32 [B, H] natural log.
  */
-int oracle_mla_decode_ref(const uint16_t* q, int64_t q_sb, int64_t q_sh, const uint16_t* kv,
+int oracle_mla_decode_ref(const void* q, int64_t q_sb, int64_t q_sh, const void* kv,
                           int64_t kv_s0, int64_t kv_s1, const int32_t* bt, int64_t bt_s0,
                           int paged, int64_t page_size, const int32_t* seqlens, int64_t batch,
                           int64_t heads, int64_t dqk, int64_t dv, int dtype, double scale,
@@ -222,8 +232,8 @@ int oracle_mla_decode_ref(const uint16_t* q, int64_t q_sb, int64_t q_sh, const u
         if (!k) return 2;
 #pragma omp parallel for schedule(static)
         for (int64_t t = 0; t < n; ++t) {
-            const uint16_t* row = kv + token_offset(b, t, bt, bt_s0, paged, page_size, kv_s0, kv_s1);
-            for (int64_t c = 0; c < dqk; ++c) k[t * dqk + c] = half_bits_to_double(row[c], dtype);
+            const int64_t row = token_offset(b, t, bt, bt_s0, paged, page_size, kv_s0, kv_s1);
+            for (int64_t c = 0; c < dqk; ++c) k[t * dqk + c] = elem_to_double(kv, row + c, dtype);
         }
         const int rc = attend_rows(k, n, q, q_sb, q_sh, b, heads, dqk, dv, dtype, scale, out, lse);
         free(k);

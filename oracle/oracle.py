@@ -38,7 +38,7 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "_build", "libmla_oracle.so")
-_DTYPE_CODE = {"bf16": 0, "fp16": 1}
+_DTYPE_CODE = {"bf16": 0, "fp16": 1, "fp32": 2}
 
 _lib = None
 
@@ -118,11 +118,19 @@ def float_to_half(x: np.ndarray, dtype: str) -> np.ndarray:
 # decode attention
 # ----------------------------------------------------------------------------
 
-def _cache_args(kv_cache: np.ndarray, block_table):
+def _elems(a: np.ndarray, dtype: str) -> np.ndarray:
+    """16-bit types travel as uint16 bit patterns, fp32 as float32 values."""
+    if dtype == "fp32":
+        assert a.dtype == np.float32, "fp32 arrays travel as float32"
+        return np.ascontiguousarray(a)
+    return np.ascontiguousarray(_u16(a))
+
+
+def _cache_args(kv_cache: np.ndarray, block_table, dtype="bf16"):
     if kv_cache.ndim == 4:  # FlashMLA layout [..., 1, D] (reference.py:8-9)
         assert kv_cache.shape[2] == 1
         kv_cache = kv_cache.reshape(kv_cache.shape[0], kv_cache.shape[1], kv_cache.shape[3])
-    kv_cache = np.ascontiguousarray(_u16(kv_cache))
+    kv_cache = _elems(kv_cache, dtype)
     if block_table is None:
         return kv_cache, None, 0, 0, 1
     bt = np.ascontiguousarray(block_table, dtype=np.int32)
@@ -133,13 +141,15 @@ def mla_decode_ref(q, kv_cache, cache_seqlens, block_table=None, head_dim_v=512,
                    softmax_scale=None, dtype="bf16", nthreads=0):
     """Restates reference.py:16-31 in float64.
 
-    Returns ``(out float32 [B, H, dv] unrounded, lse float32 [B, H])``.
+    ``dtype`` "bf16" / "fp16" (q and the cache as uint16 bit patterns) or
+    "fp32" (float32 arrays). Returns ``(out float32 [B, H, dv] unrounded,
+    lse float32 [B, H])``.
     """
-    q = np.ascontiguousarray(_u16(q))
+    q = _elems(q, dtype)
     B, H, dqk = q.shape
     if softmax_scale is None:
         softmax_scale = dqk ** -0.5  # reference.py:18-19
-    kv, bt, bt_s0, paged, page_size = _cache_args(kv_cache, block_table)
+    kv, bt, bt_s0, paged, page_size = _cache_args(kv_cache, block_table, dtype)
     assert kv.shape[-1] == dqk
     seqlens = np.ascontiguousarray(cache_seqlens, dtype=np.int32)
     out = np.empty((B, H, head_dim_v), dtype=np.float32)

@@ -2,8 +2,9 @@
 // built by tests/test_plan_sanitize.py with the address and undefined-behaviour
 // sanitizers (any signed overflow, out-of-range shift or bad access aborts).
 // It sweeps extreme batch, head, split, worker and capacity values through
-// check_common, ws_layout, worker_grid, plan_launch and plan_launch_g16 and checks the
-// invariants the kernels rely on. Prints "ok <cases>" on success.
+// check_common, ws_layout, worker_grid, plan_launch and plan_launch_g16, and the
+// generic decode's check_generic, generic_plan and generic_workspace_bytes, and checks
+// the invariants the kernels rely on. Prints "ok <cases>" on success.
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -84,6 +85,46 @@ int main() {
                 }
               }
         }
+  // the generic decode: dims, element types, shapes, workspaces
+  const int32_t gdims[] = {0, 8, 16, 24, 32, 64, 128, 256, 512, 1024, 2048, -16};
+  const int32_t gsplits[] = {-1, 0, 1, 7, 64, 65535, 65536, I32};
+  const int32_t gbatches[] = {0, 1, 65535, 65536, I32};
+  const int32_t gheads[] = {0, 1, 17, 65535, 65536, I32};
+  for (int32_t dv : gdims)
+    for (int32_t dr : gdims)
+      for (int dt = 0; dt <= 3; ++dt) {
+        const bool dims_ok = dv >= 16 && dv <= 1024 && dr >= 16 && dr <= 256 && (dv & (dv - 1)) == 0 &&
+                             (dr & (dr - 1)) == 0;
+        if (dims_ok && dt <= 2) {
+          const GenericPlan gp = generic_plan(dv, dr, dt);
+          const int64_t d = (int64_t)dv + dr;
+          EXPECT(gp.lds == kGenSmallLds || gp.lds == kGenLargeLds, "lds form");
+          EXPECT(gp.tile >= 8 && gp.tile <= 64 && (gp.tile & (gp.tile - 1)) == 0, "tile %d dv=%d dr=%d", gp.tile, dv, dr);
+          EXPECT(64 * d + kGenProbBytes + (int64_t)gp.tile * gp.pitch <= gp.lds, "LDS fits dv=%d dr=%d", dv, dr);
+          EXPECT(gp.pitch % 16 == 0 && gp.pitch == d * elem_bytes(dt) + 16, "pitch");
+          EXPECT(gp.lds <= 160 * 1024 && (gp.lds != kGenSmallLds || gp.tile >= 16), "the small form holds 16 rows");
+        }
+        for (int32_t b : gbatches)
+          for (int32_t h : gheads)
+            for (int32_t s : gsplits)
+              for (int paged = 0; paged <= 1; ++paged) {
+                ++cases;
+                const GenericCall c{b, h, dv, dr, dt, s, paged != 0, paged ? 64 : 1, 16, 1024};
+                const size_t need = generic_workspace_bytes(b, h, dv, s);
+                const bool valid = b >= 0 && b <= 65535 && h > 0 && h <= 65535 && dims_ok && dt <= 2 && s >= 1 &&
+                                   s <= 65535;
+                const int rc = check_generic(c, &dummy, need);
+                if (valid) {
+                  EXPECT(need > 0 && rc == TMLA_OK, "generic b=%d h=%d dv=%d dr=%d s=%d rc=%d", b, h, dv, dr, s, rc);
+                  const int64_t rows = (int64_t)b * h * s;
+                  EXPECT((int64_t)need >= rows * ((int64_t)dv + 1) * 4 && need % 256 == 0, "generic need");
+                  EXPECT(check_generic(c, &dummy, need - 1) == TMLA_ERR_WORKSPACE_TOO_SMALL, "generic ws-1");
+                  EXPECT(check_generic(c, nullptr, need) == TMLA_ERR_WORKSPACE_TOO_SMALL, "generic null ws");
+                } else {
+                  EXPECT(rc != TMLA_OK, "generic invalid accepted b=%d h=%d dv=%d dr=%d dt=%d s=%d", b, h, dv, dr, dt, s);
+                }
+              }
+      }
   if (failures) {
     fprintf(stderr, "%d failures\n", failures);
     return 1;

@@ -109,6 +109,45 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert b"null" in lib.tmla_last_error()
 
 
+def _generic(lib, **kw):
+    args = dict(q=None, qsb=160 * 16, qsh=160, kv=None, kv0=64 * 160, kv1=160, nblocks=64, page=1,
+                bt=None, btsb=1, btcols=1, seqlens=None, batch=2, heads=16, dv=128, dr=32, dtype=2,
+                scale=0.1, splits=2, out=None, osb=16 * 128, osh=128, lse=None, ws=None, wsb=0, stream=None)
+    args.update(kw)
+    return lib.tmla_mla_decode_generic(*args.values())
+
+
+def test_generic_workspace_and_rejections(lib):
+    # float32 partial rows [batch, heads, splits, dv], then their lse values,
+    # each 256-byte aligned, plus 256 bytes (so an empty batch needs a buffer too)
+    assert lib.tmla_generic_workspace_bytes(2, 16, 128, 2) == _al(64 * 128 * 4) + _al(64 * 4) + 256
+    assert lib.tmla_generic_workspace_bytes(3, 5, 16, 7) == _al(105 * 16 * 4) + _al(105 * 4) + 256
+    assert lib.tmla_generic_workspace_bytes(0, 5, 16, 7) == 256
+    assert lib.tmla_generic_workspace_bytes(2, 16, 128, 0) == 0
+    assert lib.tmla_generic_workspace_bytes(2, 0, 128, 1) == 0
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    ws = lib.tmla_generic_workspace_bytes(2, 16, 128, 2)
+    assert _generic(lib, dtype=3, ws=fake, wsb=ws) == 1
+    assert b"dtype" in lib.tmla_last_error()
+    for dv, dr in [(96, 32), (2048, 64), (128, 8), (128, 512), (8, 16), (128, 0)]:
+        assert _generic(lib, dv=dv, dr=dr, ws=fake, wsb=ws) == 2, (dv, dr)
+    assert _generic(lib, splits=0, ws=fake, wsb=ws) == 1
+    assert _generic(lib, splits=65536, ws=fake, wsb=1 << 40) == 1
+    assert _generic(lib, batch=65536, ws=fake, wsb=1 << 40) == 2
+    assert _generic(lib, heads=0, ws=fake, wsb=ws) == 1
+    assert _generic(lib, ws=fake, wsb=ws - 1) == 3
+    assert _generic(lib, ws=None, wsb=0) == 3
+    assert _generic(lib, page=64, ws=fake, wsb=ws) == 1  # a dense cache has page_size 1
+    assert _generic(lib, bt=fake, page=0, ws=fake, wsb=ws) == 1  # a paged one at least 1
+    assert _generic(lib, bt=fake, page=16, nblocks=0, ws=fake, wsb=ws) == 1
+    assert _generic(lib, batch=0, ws=fake, wsb=256) == 0  # nothing to do
+    # null tensors are caught before any launch
+    assert _generic(lib, ws=fake, wsb=ws) == 1
+    assert b"NULL" in lib.tmla_last_error()
+    # the matrix-core entry points keep refusing float32
+    assert _partial(lib, dtype=2, ws=fake, wsb=lib.tmla_workspace_bytes(2, 128, 512, 1, 0)) == 1
+
+
 def test_layer_glue_arguments_rejected_on_host(lib):
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
     # tmla_mla_absorb_q(q_proj, q_sb, wkv_b, w_s0, positions, batch, heads, nope, rope, rank, vd, theta,

@@ -46,6 +46,49 @@ def test_cpu_tensors_are_refused_loudly():
         mla_decode(q, kv, lens)
 
 
+def test_other_dims_and_fp32_take_the_generic_path():
+    """head_dim_v / rope_dim other than 512 / 64, or fp32 inputs, go to the
+    generic decode: the reference's assertions first, then its limits, then the
+    same loud refusal of CPU tensors."""
+    from triton_mla import mla_decode
+
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(2, 4, 160, generator=g)
+    kv = torch.randn(2, 40, 160, generator=g)
+    lens = torch.tensor([40, 3], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        mla_decode(q, kv, lens, head_dim_v=128)  # fp32, 128 + 32
+    with pytest.raises(RuntimeError, match="GPU only"):
+        mla_decode(q.to(torch.bfloat16), kv.to(torch.bfloat16), lens, head_dim_v=128)
+    qf, kvf = torch.randn(2, 4, D, generator=g), torch.randn(2, 40, D, generator=g)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        mla_decode(qf, kvf, lens)  # fp32 at 512 + 64
+    with pytest.raises(AssertionError):
+        mla_decode(q, kv, lens, head_dim_v=100)  # not a power of two
+    with pytest.raises(AssertionError):
+        mla_decode(q, kv.to(torch.float16), lens, head_dim_v=128)  # dtype mismatch
+    with pytest.raises(NotImplementedError, match="rope_dim"):
+        mla_decode(q[..., :136].contiguous(), kv[..., :136].contiguous(), lens, head_dim_v=128)  # rope 8
+    with pytest.raises(NotImplementedError, match="head_dim_v"):
+        mla_decode(torch.randn(2, 4, 2112), torch.randn(2, 40, 2112), lens, head_dim_v=2048)
+    with pytest.raises(NotImplementedError, match="fp32"):
+        mla_decode(q.double(), kv.double(), lens, head_dim_v=128)
+    with pytest.raises(NotImplementedError, match="multi-token"):
+        mla_decode(q.unsqueeze(1), kv, lens, head_dim_v=128)
+
+
+def test_generic_default_splits():
+    """About four 16-head workgroups per compute unit, pieces of >= 256 tokens."""
+    from triton_mla.kernel import _generic_splits
+
+    assert _generic_splits(32, 128, 8192, 256) == 4  # 256 workgroup groups
+    assert _generic_splits(64, 16, 16384, 256) == 16
+    assert _generic_splits(1, 16, 1000, 256) == 4  # capped by the length: cdiv(1000, 256)
+    assert _generic_splits(1, 16, 0, 256) == 1
+    assert _generic_splits(4096, 128, 1 << 20, 256) == 1
+    assert _generic_splits(1, 1, 1 << 30, 1 << 20) == 65535
+
+
 def test_torch_reference_functions_match_oracle():
     """The package's mla_decode_ref / mla_decode_torch / gather_kv (torch API,
     reference.py:6-44) against the float64 oracle on the CPU."""

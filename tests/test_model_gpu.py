@@ -56,6 +56,36 @@ def test_absorbed_decode_matches_naive(gpu, paged):
     torch.testing.assert_close(out.float(), ref.float(), atol=3e-2, rtol=3e-2)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_other_dims_and_fp32_layer_matches_naive(gpu, dtype):
+    """A layer outside the HIP glue's dims (latent 256, rope 32, nope 64, value
+    64) and the reference test's fp32 layer (tests/test_model.py:34: atol 1e-4
+    in fp32): the torch glue around the generic decode against the
+    non-absorbed step."""
+    from triton_mla import MLAConfig
+
+    gen = torch.Generator().manual_seed(4)
+    cfgs = [MLAConfig(hidden_size=256, num_heads=16, q_lora_rank=128, kv_lora_rank=256, qk_nope_head_dim=64,
+                      qk_rope_head_dim=32, v_head_dim=64)]
+    if dtype == torch.float32:
+        cfgs.append(MLAConfig(hidden_size=256, num_heads=16, q_lora_rank=128))
+    for cfg in cfgs:
+        model = _model(cfg, gen).to(gpu, dtype)
+        batch, max_len, page_size = 3, 256, 16
+        seqlens = torch.tensor([0, 5, max_len // 2], dtype=torch.int32, device=gpu)
+        blocks = max_len // page_size
+        block_table = torch.randperm(batch * blocks, generator=gen).view(batch, blocks).int().to(gpu)
+        kv_cache = torch.randn(batch * blocks, page_size, cfg.kv_cache_dim, generator=gen).to(gpu, dtype)
+        x = torch.randn(batch, cfg.hidden_size, generator=gen).to(gpu, dtype)
+        cache_a, cache_b = kv_cache.clone(), kv_cache.clone()
+        with torch.no_grad():
+            out, new_lens = model(x, cache_a, seqlens, block_table)
+            ref, _ = model.forward_naive(x, cache_b, seqlens, block_table)
+        assert torch.equal(new_lens, seqlens + 1)
+        tol = 1e-4 if dtype == torch.float32 else 3e-2
+        torch.testing.assert_close(out.float(), ref.float(), atol=tol, rtol=tol)
+
+
 def test_absorbed_decode_matches_layer_oracle(gpu):
     from triton_mla import MLAConfig
 

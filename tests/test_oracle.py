@@ -235,6 +235,49 @@ def test_fp16_inputs():
 
 
 # ---------------------------------------------------------------------------
+# other head dims and float32 elements (what the generic decode is checked by)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dv,dr", [(16, 16), (128, 32), (1024, 256)])
+def test_decode_ref_other_dims_fp32(dv, dr):
+    """float32 elements at other dims: scipy's softmax/logsumexp, the
+    one-token closed form and an empty sequence."""
+    rng = np.random.default_rng(dv + dr)
+    d = dv + dr
+    q = rng.standard_normal((2, 5, d)).astype(np.float32)
+    kv = rng.standard_normal((2, 23, d)).astype(np.float32)
+    out, lse = oracle.mla_decode_ref(q, kv, np.array([23, 0], np.int32), None, dv, 0.07, dtype="fp32")
+    s = q[0].astype(np.float64) @ kv[0].astype(np.float64).T * 0.07
+    np.testing.assert_allclose(out[0], softmax(s, -1) @ kv[0, :, :dv].astype(np.float64), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(lse[0], logsumexp(s, -1), rtol=1e-6, atol=1e-6)
+    assert np.all(out[1] == 0) and np.all(np.isneginf(lse[1]))
+    out1, lse1 = oracle.mla_decode_ref(q, kv, np.array([1, 1], np.int32), None, dv, 0.07, dtype="fp32")
+    assert np.array_equal(out1, np.broadcast_to(kv[:, None, 0, :dv], out1.shape))
+    sc = (q.astype(np.float64) * kv[:, None, 0, :].astype(np.float64)).sum(-1) * 0.07
+    np.testing.assert_allclose(lse1, sc, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_decode_ref_fp32_equals_bf16_on_shared_values(paged):
+    """bf16 values handed over as float32 give the bf16 oracle's results bit
+    for bit, dense and through a block table (the element loader is the only
+    difference between the two)."""
+    rng = np.random.default_rng(11)
+    dv, d = 128, 160
+    q = rand_bits(rng, (3, 4, d))
+    kv = rand_bits(rng, (3, 32, d))
+    n = np.array([30, 17, 0], np.int32)
+    bt = None
+    if paged:
+        kv = kv.reshape(3 * 4, 8, d)[rng.permutation(12)]
+        bt = rng.permutation(12).astype(np.int32).reshape(3, 4)
+    a = oracle.mla_decode_ref(q, kv, n, bt, dv, 0.1, dtype="bf16")
+    b = oracle.mla_decode_ref(as_f64(q).astype(np.float32), as_f64(kv).astype(np.float32), n, bt, dv, 0.1,
+                              dtype="fp32")
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+# ---------------------------------------------------------------------------
 # planted mistakes: the checks above must reject a wrong algorithm
 # ---------------------------------------------------------------------------
 

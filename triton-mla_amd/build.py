@@ -37,7 +37,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "triton_mla", "libtriton_mla_hip.so")
 LIB_STAMPS = os.path.join(HERE, "triton_mla", "libtriton_mla_hip_stamps.so")
-SOURCES = ["mla_decode.hip", "mla_decode_fp8.hip", "mla_decode_g16.hip", "mla_layer.hip"]
+SOURCES = ["mla_decode.hip", "mla_decode_fp8.hip", "mla_decode_g16.hip", "mla_decode_generic.hip", "mla_layer.hip"]
 ARCH = os.environ.get("TRITON_MLA_ARCH", "gfx950")
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-mcode-object-version=5",

@@ -174,4 +174,93 @@ inline int check_common(const Common& c, const void* workspace, size_t ws_bytes)
   return TMLA_OK;
 }
 
+// ---------------------------------------------------------------------------
+// The generic decode: head dims and element types outside the specialised
+// kernels (any power-of-two head_dim_v in [16, 1024] and rope_dim in
+// [16, 256]; bf16, fp16 or fp32), with the reference's uniform splits and
+// float32 partials [batch, heads, splits, dv] plus their base-2 lse
+// [batch, heads, splits].
+// ---------------------------------------------------------------------------
+constexpr int kGenHeads = 16;                   // heads per workgroup (4 per wave)
+constexpr int kGenSmallLds = 64 * 1024;         // two workgroups per compute unit
+constexpr int kGenLargeLds = 152 * 1024;        // one
+constexpr int kGenProbBytes = 4 * 64 * 4 * 4;   // probabilities: [waves][tokens][4 heads] float
+constexpr int kGenMaxSplits = 65535;            // grid.y of the partial kernel
+constexpr int kGenMaxBatchHeads = 65535;        // grid.z of the partial kernel, grid.y of the merge
+
+inline bool pow2_between(int64_t x, int64_t lo, int64_t hi) { return x >= lo && x <= hi && (x & (x - 1)) == 0; }
+inline int elem_bytes(int32_t dtype) { return dtype == TMLA_FP32 ? 4 : 2; }
+
+struct GenericPlan {
+  int lds;    // LDS bytes of the kernel form (kGenSmallLds or kGenLargeLds)
+  int tile;   // tokens staged per step: a power of two in [1, 64]
+  int pitch;  // LDS bytes per staged row: the row plus 16 bytes of padding
+};
+
+// LDS of a workgroup: Q of its heads in float (64 * D bytes), the
+// probabilities, and `tile` rows. The small form when it holds at least 16
+// rows. Valid for dims accepted by check_generic (D <= 1280: the large form
+// holds at least 8 fp32 rows beside Q).
+inline GenericPlan generic_plan(int32_t dv, int32_t dr, int32_t dtype) {
+  const int64_t d = (int64_t)dv + dr;
+  GenericPlan p;
+  p.pitch = (int)(d * elem_bytes(dtype) + 16);
+  auto tile_in = [&](int lds) {
+    const int64_t room = lds - 64 * d - kGenProbBytes;
+    int t = 64;
+    while (t > 0 && (int64_t)t * p.pitch > room) t >>= 1;
+    return t;
+  };
+  const int small = tile_in(kGenSmallLds);
+  if (small >= 16) {
+    p.lds = kGenSmallLds;
+    p.tile = small;
+  } else {
+    p.lds = kGenLargeLds;
+    p.tile = tile_in(kGenLargeLds);
+  }
+  return p;
+}
+
+// Workspace of a generic call: the float32 partial rows, then their lse
+// values (both 256-byte aligned); 0 for invalid or too large arguments.
+inline size_t generic_workspace_bytes(int32_t batch, int32_t heads, int32_t dv, int32_t splits) {
+  if (batch < 0 || heads <= 0 || dv <= 0 || splits <= 0) return 0;
+  int64_t rows = (int64_t)batch * heads;  // below 2^62
+  if (rows > 0 && splits > kMaxWorkspaceBytes / rows) return 0;
+  rows *= splits;
+  if (rows > 0 && ((int64_t)dv + 1) * 4 > kMaxWorkspaceBytes / rows) return 0;
+  auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
+  const int64_t total = al(rows * dv * 4) + al(rows * 4) + 256;
+  return total > kMaxWorkspaceBytes ? 0 : (size_t)total;
+}
+
+struct GenericCall {
+  int32_t batch, heads, dv, dr, dtype, splits;
+  bool paged;
+  int32_t page_size, bt_cols;
+  int64_t num_blocks;
+};
+
+inline int check_generic(const GenericCall& c, const void* workspace, size_t ws_bytes) {
+  if (c.batch < 0 || c.heads <= 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "batch must be >= 0 and num_heads > 0");
+  if (c.dtype != TMLA_BF16 && c.dtype != TMLA_FP16 && c.dtype != TMLA_FP32)
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "dtype must be TMLA_BF16, TMLA_FP16 or TMLA_FP32");
+  if (!pow2_between(c.dv, 16, 1024) || !pow2_between(c.dr, 16, 256))
+    return fail(TMLA_ERR_UNSUPPORTED,
+                "head_dim_v must be a power of two in [16, 1024] and rope_dim a power of two in [16, 256]");
+  if (c.splits < 1 || c.splits > kGenMaxSplits) return fail(TMLA_ERR_INVALID_ARGUMENT, "num_splits must be in [1, 65535]");
+  if (c.batch > kGenMaxBatchHeads || c.heads > kGenMaxBatchHeads)
+    return fail(TMLA_ERR_UNSUPPORTED, "batch and num_heads must be at most 65535");
+  if (c.paged && (c.page_size < 1 || c.bt_cols < 1 || c.num_blocks < 1))
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "a paged cache needs page_size, bt_cols and num_blocks >= 1");
+  if (!c.paged && (c.page_size != 1 || c.num_blocks < 0))
+    return fail(TMLA_ERR_INVALID_ARGUMENT, "a dense cache needs page_size 1 and num_blocks (its capacity) >= 0");
+  const size_t need = generic_workspace_bytes(c.batch, c.heads, c.dv, c.splits);
+  if (need == 0) return fail(TMLA_ERR_INVALID_ARGUMENT, "the call's workspace would exceed 2^62 bytes");
+  if (workspace == nullptr || ws_bytes < need)
+    return fail(TMLA_ERR_WORKSPACE_TOO_SMALL, "workspace is missing or smaller than tmla_generic_workspace_bytes()");
+  return TMLA_OK;
+}
+
 }  // namespace tmla

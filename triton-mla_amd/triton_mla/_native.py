@@ -54,6 +54,10 @@ SIGNATURES = {
     "tmla_mla_decode_fp8": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
         _i32, _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "tmla_generic_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
+    "tmla_mla_decode_generic": (ctypes.c_int, [
+        _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _f32,
+        _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "tmla_mla_decode_fp8_partial": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _i32,
         _i32, _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
@@ -72,7 +76,7 @@ SIGNATURES = {
 
 STATUS = {0: "TMLA_OK", 1: "TMLA_ERR_INVALID_ARGUMENT", 2: "TMLA_ERR_UNSUPPORTED",
           3: "TMLA_ERR_WORKSPACE_TOO_SMALL", 4: "TMLA_ERR_HIP"}
-DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1}
+DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 _lib = None
 _lock = threading.Lock()

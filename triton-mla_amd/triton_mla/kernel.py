@@ -418,6 +418,11 @@ def mla_decode(
         out [batch, num_heads, head_dim_v] in q.dtype (and lse [batch,
         num_heads] float32).
     """
+    if q.dtype == torch.float32 or head_dim_v != 512 or q.shape[-1] != 576:
+        if kv_scale is not None:
+            raise NotImplementedError("an fp8 kv_cache is supported at head_dim_v=512, rope_dim=64")
+        return _generic_decode(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits,
+                               return_lse)
     single = DEFAULT_SINGLE_LAUNCH if single_launch is None else bool(single_launch)
     if not single and kv_scale is None:
         res = _fast_call(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits, return_lse)
@@ -426,6 +431,94 @@ def mla_decode(
     call = DecodeLaunch(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits,
                         kv_scale=kv_scale)
     out, lse = call.run(single)
+    if return_lse:
+        return out, lse
+    return out
+
+
+_GENERIC_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def _generic_splits(batch, num_heads, capacity, num_sms):
+    """Default split count of the generic decode: about four workgroups (16
+    heads, one piece of a sequence) per compute unit, pieces of at least 256
+    tokens of the cache's capacity, at most 65535 (the launch's grid.y)."""
+    groups = max(batch * -(-num_heads // 16), 1)
+    by_cus = -(-4 * num_sms // groups)
+    by_len = max(-(-capacity // 256), 1)
+    return max(1, min(by_cus, by_len, 65535))
+
+
+def _generic_decode(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits, return_lse):
+    """``mla_decode`` at head dims or an element type the matrix-core kernels
+    are not built for (tmla_mla_decode_generic): any power-of-two head_dim_v
+    in [16, 1024] and rope_dim in [16, 256], bf16, fp16 or fp32 -- the
+    reference's kernels take powers of two and any dtype q and the cache
+    share (kernel.py:243-245). Both of the reference's stages with its
+    uniform splits (kernel.py:84-86) and float32 partials; ``num_splits=None``
+    takes _generic_splits of the cache's capacity (sized for this kernel's
+    16-head workgroups; no call reads ``cache_seqlens`` back to the host).
+    Vector ALU kernels: meant for unusual dims, not for speed."""
+    # validation mirrors kernel.py:235-245
+    if kv_cache.dim() == 4:
+        assert kv_cache.shape[2] == 1, "MLA uses a single shared latent KV head"
+        kv_cache = kv_cache.squeeze(2)
+    if q.dim() == 4:
+        raise NotImplementedError("multi-token queries are supported at head_dim_v=512, rope_dim=64 in bf16/fp16")
+    assert q.dim() == 3 and kv_cache.dim() == 3
+    batch, num_heads, d_qk = q.shape
+    d_rope = d_qk - head_dim_v
+    assert kv_cache.shape[-1] == d_qk
+    assert q.stride(-1) == 1 and kv_cache.stride(-1) == 1
+    assert _next_power_of_2(head_dim_v) == head_dim_v
+    assert _next_power_of_2(d_rope) == d_rope
+    assert q.dtype == kv_cache.dtype
+    if q.dtype not in _GENERIC_DTYPES:
+        raise NotImplementedError(f"mla_decode supports bf16, fp16 and fp32 inputs, got {q.dtype}")
+    if not (16 <= head_dim_v <= 1024 and 16 <= d_rope <= 256):
+        raise NotImplementedError(f"mla_decode supports head_dim_v in [16, 1024] and rope_dim in [16, 256] "
+                                  f"(powers of two); got {head_dim_v}, {d_rope}")
+    if q.device.type != "cuda" or kv_cache.device != q.device:
+        raise RuntimeError("triton_mla.mla_decode runs on the GPU only: q and kv_cache must be "
+                           "on the same HIP device")
+    if softmax_scale is None:
+        softmax_scale = d_qk ** -0.5  # kernel.py:247-248
+    device = q.device
+    cache_seqlens = cache_seqlens.to(device=device, dtype=torch.int32).contiguous()
+    assert cache_seqlens.shape == (batch,), "cache_seqlens must be [batch]"
+    if block_table is not None:
+        block_table = block_table.to(device=device, dtype=torch.int32)
+        if block_table.stride(-1) != 1:
+            block_table = block_table.contiguous()
+        assert block_table.dim() == 2 and block_table.shape[0] == batch
+        page_size, num_blocks = kv_cache.shape[1], kv_cache.shape[0]
+        capacity = block_table.shape[1] * page_size
+        bt_args = (block_table.data_ptr(), block_table.stride(0), block_table.shape[1])
+    else:
+        assert kv_cache.shape[0] == batch  # kernel.py:258
+        page_size, num_blocks = 1, kv_cache.shape[1]
+        capacity = num_blocks
+        bt_args = (None, 0, 1)
+    if num_splits is None:
+        num_splits = _generic_splits(batch, num_heads, capacity, _num_sms(device))
+    num_splits = int(num_splits)
+    assert num_splits >= 1, "num_splits must be >= 1"
+    out = torch.empty(batch, num_heads, head_dim_v, dtype=q.dtype, device=device)
+    lse = torch.empty(batch, num_heads, dtype=torch.float32, device=device)
+    if batch:
+        if block_table is not None and num_blocks == 0:
+            raise ValueError("kv_cache holds no pages")
+        lib = _native.load()
+        ws_bytes = lib.tmla_generic_workspace_bytes(batch, num_heads, head_dim_v, num_splits)
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+        dev_idx = device.index if device.index is not None else torch.cuda.current_device()
+        with _OnDevice(dev_idx):
+            _native.check(lib.tmla_mla_decode_generic(
+                q.data_ptr(), q.stride(0), q.stride(1), kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1),
+                num_blocks, page_size, *bt_args, cache_seqlens.data_ptr(), batch, num_heads, head_dim_v, d_rope,
+                _native.DTYPE_CODE[q.dtype], float(softmax_scale), num_splits, out.data_ptr(), out.stride(0),
+                out.stride(1), lse.data_ptr(), workspace.data_ptr(), ws_bytes,
+                torch.cuda.current_stream(device).cuda_stream), "tmla_mla_decode_generic")
     if return_lse:
         return out, lse
     return out

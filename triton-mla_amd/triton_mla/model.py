@@ -80,6 +80,15 @@ def apply_rope(x, positions, theta):
     return rotated.to(x.dtype)
 
 
+def _hip_glue_dims(cfg) -> bool:
+    """Dims the HIP layer kernels are built for: q_pe RoPE and W_UK absorption
+    at nope 128 / rope 64, the latent a multiple of 512 up to 1024, W_UV
+    blocks of 32 value dims, q_lora_rank a multiple of 8 (DeepSeek V2, V2-Lite
+    and V3 all fit)."""
+    return (cfg.qk_nope_head_dim == 128 and cfg.qk_rope_head_dim == 64 and cfg.kv_lora_rank % 512 == 0
+            and cfg.kv_lora_rank <= 1024 and cfg.v_head_dim % 32 == 0 and cfg.q_lora_rank % 8 == 0)
+
+
 class MLA(nn.Module):
     """Multi-head Latent Attention: per token only the compressed latent
     (kv_lora_rank) and the shared RoPE key (qk_rope_head_dim) are cached."""
@@ -147,9 +156,10 @@ class MLA(nn.Module):
         (output [batch, hidden], updated cache_seqlens).
         """
         cfg = self.cfg
-        if kv_cache.dtype != x.dtype or x.dtype not in (torch.bfloat16, torch.float16):
-            # the HIP glue runs in the layer's 16-bit dtype; other dtype mixes
-            # take the reference's torch glue, which casts (model.py:108-124)
+        if kv_cache.dtype != x.dtype or x.dtype not in (torch.bfloat16, torch.float16) or not _hip_glue_dims(cfg):
+            # the HIP glue runs in the layer's 16-bit dtype at the DeepSeek
+            # head dims; other dtype mixes and dims take the reference's torch
+            # glue, which casts (model.py:108-124), around the same mla_decode
             return self.forward_torch_glue(x, kv_cache, cache_seqlens, block_table, num_splits)
         q_lat, kv_proj = self._down_proj(x)  # [B, q_lora_rank], [B, rank + rope]
         # in one launch: q_norm (model.py:76); RMSNorm(c_kv), RoPE(k_pe) and
