@@ -418,16 +418,16 @@ def mla_decode(
         out [batch, num_heads, head_dim_v] in q.dtype (and lse [batch,
         num_heads] float32).
     """
-    if q.dtype == torch.float32 or head_dim_v != 512 or q.shape[-1] != 576:
-        if kv_scale is not None:
-            raise NotImplementedError("an fp8 kv_cache is supported at head_dim_v=512, rope_dim=64")
-        return _generic_decode(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits,
-                               return_lse)
     single = DEFAULT_SINGLE_LAUNCH if single_launch is None else bool(single_launch)
     if not single and kv_scale is None:
         res = _fast_call(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits, return_lse)
         if res is not None:
             return res if return_lse else res[0]
+    if q.dtype == torch.float32 or head_dim_v != 512 or q.shape[-1] != 576:
+        if kv_scale is not None:
+            raise NotImplementedError("an fp8 kv_cache is supported at head_dim_v=512, rope_dim=64")
+        return _generic_decode(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits,
+                               return_lse)
     call = DecodeLaunch(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits,
                         kv_scale=kv_scale)
     out, lse = call.run(single)
@@ -604,7 +604,8 @@ def _learn_shape(key, q, kv_cache, cache_seqlens, block_table, head_dim_v, softm
     constant arguments; False (kept too) when the fast path does not apply
     to the shape. q and kv_cache are 16-byte aligned here."""
     shape = False
-    if q.dim() == 3 and kv_cache.dtype in _DTYPES and cache_seqlens.dtype == torch.int32 \
+    if q.dim() == 3 and kv_cache.dtype in _DTYPES and head_dim_v == 512 and q.shape[-1] == 576 \
+            and cache_seqlens.dtype == torch.int32 \
             and cache_seqlens.device == q.device and cache_seqlens.is_contiguous() \
             and (block_table is None or (block_table.dtype == torch.int32 and block_table.device == q.device
                                          and block_table.dim() == 2 and block_table.stride(-1) == 1)):
