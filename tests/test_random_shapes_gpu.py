@@ -1,0 +1,76 @@
+"""Randomised shapes through the public ``mla_decode`` against the float64
+oracle: 128 draws from a fixed seed of batch (1-12), heads (1-260: every
+kernel and head-block form, partial head blocks), sequence lengths (empty,
+one token, not multiples of the 32-token sub-tile or the 64-token tile, up to
+3,000), dense or paged caches (pages of 16-256 tokens, shuffled tables with
+spare columns), the balanced partition or 1-24 uniform splits, bf16 or fp16,
+the single launch or two kernels. Each call is checked at the parity bar
+(out atol = rtol = 1e-2, lse 1e-3 on non-empty rows, empty sequences exactly
+0 and -inf) and against the other launch form bit for bit.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import bits, dtype_name
+
+pytestmark = pytest.mark.gpu
+
+D, DV = 576, 512
+
+
+def _draw(seed):
+    rng = np.random.default_rng(1000 + seed)
+    batch = int(rng.integers(1, 13))
+    heads = int(rng.choice([1, 3, 8, 16, 17, 31, 32, 33, 48, 64, 65, 96, 127, 128, 129, 200, 256, 260]))
+    max_len = int(rng.integers(1, 3001))
+    lens = rng.integers(0, max_len + 1, size=batch)
+    specials = [0, 1, max_len, 31, 33, 63, 65]
+    for i in range(min(batch, int(rng.integers(0, 4)))):
+        lens[i] = min(int(rng.choice(specials)), max_len)
+    page = int(rng.choice([0, 16, 32, 64, 128, 256]))
+    splits = None if rng.random() < 0.5 else int(rng.integers(1, 25))
+    dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float16
+    return batch, heads, max_len, lens.astype(np.int32), page, splits, dtype
+
+
+@pytest.mark.parametrize("seed", range(128))
+def test_random_shape(gpu, seed):
+    import triton_mla
+
+    batch, heads, max_len, lens, page, splits, dtype = _draw(seed)
+    print(f"seed {seed}: batch={batch} heads={heads} max_len={max_len} page={page} splits={splits} "
+          f"{dtype_name(dtype)}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, heads, D, generator=g).to(dtype)
+    kv = torch.randn(batch, max_len, D, generator=g).to(dtype)
+    bt = None
+    if page:
+        per_seq = -(-max_len // page) + 1  # one spare column per row
+        blocks = batch * per_seq
+        bt = torch.randperm(blocks, generator=g).view(batch, per_seq).int()
+        padded = torch.zeros(batch, per_seq * page, D, dtype=dtype)
+        padded[:, :max_len] = kv
+        cache = torch.empty(blocks, page, D, dtype=dtype)
+        cache[bt.long()] = padded.view(batch, per_seq, page, D)
+    else:
+        cache = kv
+    seqlens = torch.from_numpy(lens)
+    scale = 192 ** -0.5
+    args = (q.to(gpu), cache.to(gpu), seqlens.to(gpu), None if bt is None else bt.to(gpu))
+    two = triton_mla.mla_decode(*args, softmax_scale=scale, num_splits=splits, return_lse=True,
+                                single_launch=False)
+    one = triton_mla.mla_decode(*args, softmax_scale=scale, num_splits=splits, return_lse=True,
+                                single_launch=True)
+    torch.cuda.synchronize()
+    assert torch.equal(two[0].view(torch.int16), one[0].view(torch.int16))
+    assert torch.equal(two[1], one[1])
+    ref_out, ref_lse = oracle.mla_decode_ref(bits(q), bits(cache), lens, None if bt is None else bt.numpy(), DV,
+                                             scale, dtype=dtype_name(dtype))
+    out, lse = two[0].float().cpu(), two[1].cpu()
+    torch.testing.assert_close(out, torch.from_numpy(ref_out), atol=1e-2, rtol=1e-2)
+    valid = torch.from_numpy(lens > 0)
+    torch.testing.assert_close(lse[valid], torch.from_numpy(ref_lse)[valid], atol=1e-3, rtol=1e-3)
+    assert torch.all(out[~valid] == 0) and torch.all(torch.isneginf(lse[~valid]))
