@@ -6,7 +6,9 @@ one token, not multiples of the 32-token sub-tile or the 64-token tile, up to
 spare columns), the balanced partition or 1-24 uniform splits, bf16 or fp16,
 the single launch or two kernels. Each call is checked at the parity bar
 (out atol = rtol = 1e-2, lse 1e-3 on non-empty rows, empty sequences exactly
-0 and -inf) and against the other launch form bit for bit.
+0 and -inf) and against the other launch form bit for bit. The same draws
+also run over an fp8 cache (against the fp8 oracle) and with 1-8 query
+tokens per sequence (against the causal oracle).
 """
 
 import numpy as np
@@ -74,3 +76,81 @@ def test_random_shape(gpu, seed):
     valid = torch.from_numpy(lens > 0)
     torch.testing.assert_close(lse[valid], torch.from_numpy(ref_lse)[valid], atol=1e-3, rtol=1e-3)
     assert torch.all(out[~valid] == 0) and torch.all(torch.isneginf(lse[~valid]))
+
+
+def _paged_cache(kv, page, g):
+    batch, max_len, _ = kv.shape
+    per_seq = -(-max_len // page) + 1
+    blocks = batch * per_seq
+    bt = torch.randperm(blocks, generator=g).view(batch, per_seq).int()
+    padded = torch.zeros(batch, per_seq * page, D, dtype=kv.dtype)
+    padded[:, :max_len] = kv
+    cache = torch.empty(blocks, page, D, dtype=kv.dtype)
+    cache[bt.long()] = padded.view(batch, per_seq, page, D)
+    return cache, bt
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_shape_fp8_cache(gpu, seed):
+    """The same draws over an fp8 cache (scales per page, per token or per
+    tensor), against the float64 fp8 oracle at the parity bar."""
+    import triton_mla
+    from triton_mla import quantize_kv_fp8
+
+    batch, heads, max_len, lens, page, splits, dtype = _draw(500 + seed)
+    gran = ("page", "token", "tensor")[seed % 3]
+    print(f"fp8 seed {seed}: batch={batch} heads={heads} max_len={max_len} page={page} splits={splits} "
+          f"{gran} {dtype_name(dtype)}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, heads, D, generator=g).to(dtype)
+    kv = torch.randn(batch, max_len, D, generator=g).to(torch.bfloat16)
+    bt = None
+    if page:
+        kv, bt = _paged_cache(kv, page, g)
+    codes, scale = quantize_kv_fp8(kv, gran)
+    sm = 192 ** -0.5
+    out, lse = triton_mla.mla_decode(q.to(gpu), codes.to(gpu), torch.from_numpy(lens).to(gpu),
+                                     None if bt is None else bt.to(gpu), softmax_scale=sm, num_splits=splits,
+                                     return_lse=True, kv_scale=scale.to(gpu))
+    torch.cuda.synchronize()
+    ref_out, ref_lse = oracle.mla_decode_fp8_ref(bits(q), codes.view(torch.uint8).numpy(), scale.numpy(), lens,
+                                                 None if bt is None else bt.numpy(), DV, sm, dtype=dtype_name(dtype))
+    out, lse = out.float().cpu(), lse.cpu()
+    torch.testing.assert_close(out, torch.from_numpy(ref_out), atol=1e-2, rtol=1e-2)
+    valid = torch.from_numpy(lens > 0)
+    torch.testing.assert_close(lse[valid], torch.from_numpy(ref_lse)[valid], atol=1e-3, rtol=1e-3)
+    assert torch.all(out[~valid] == 0) and torch.all(torch.isneginf(lse[~valid]))
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_shape_multi_token(gpu, seed):
+    """The same draws with 1-8 query tokens per sequence (causal over the new
+    tokens), both launch forms bit-equal, against the float64 causal oracle."""
+    import triton_mla
+
+    batch, heads, max_len, lens, page, splits, dtype = _draw(900 + seed)
+    q_len = 1 + seed % 8
+    heads = max(1, min(heads, 512 // q_len))
+    print(f"causal seed {seed}: batch={batch} q_len={q_len} heads={heads} max_len={max_len} page={page} "
+          f"splits={splits} {dtype_name(dtype)}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, q_len, heads, D, generator=g).to(dtype)
+    kv = torch.randn(batch, max_len, D, generator=g).to(dtype)
+    bt = None
+    if page:
+        kv, bt = _paged_cache(kv, page, g)
+    sm = 192 ** -0.5
+    args = (q.to(gpu), kv.to(gpu), torch.from_numpy(lens).to(gpu), None if bt is None else bt.to(gpu))
+    two = triton_mla.mla_decode(*args, softmax_scale=sm, num_splits=splits, return_lse=True, single_launch=False)
+    one = triton_mla.mla_decode(*args, softmax_scale=sm, num_splits=splits, return_lse=True, single_launch=True)
+    torch.cuda.synchronize()
+    assert two[0].shape == (batch, q_len, heads, DV) and two[1].shape == (batch, q_len, heads)
+    assert torch.equal(two[0].view(torch.int16), one[0].view(torch.int16)) and torch.equal(two[1], one[1])
+    ref_out, ref_lse = oracle.mla_decode_ref_causal(bits(q), bits(kv), lens, None if bt is None else bt.numpy(),
+                                                    DV, sm, dtype=dtype_name(dtype))
+    out, lse = two[0].float().cpu(), two[1].cpu()
+    torch.testing.assert_close(out, torch.from_numpy(ref_out), atol=1e-2, rtol=1e-2)
+    seen = torch.from_numpy(lens[:, None] - (q_len - 1 - np.arange(q_len))[None, :] > 0)  # [B, T]
+    seen = seen[:, :, None].expand(batch, q_len, heads)
+    torch.testing.assert_close(lse[seen], torch.from_numpy(ref_lse)[seen], atol=1e-3, rtol=1e-3)
+    assert torch.all(out[~seen] == 0) and torch.all(torch.isneginf(lse[~seen]))
