@@ -303,14 +303,24 @@ int tmla_mla_decode_fp8_partial(const void* q, int64_t q_stride_b, int64_t q_str
  * log-sum-exp (kernel.py:43-138, launch kernel.py:276-302), which a second
  * kernel merges (kernel.py:141-181, launch kernel.py:303-320). Scores and
  * sums in float32, probabilities rounded to dtype for the value product
- * (kernel.py:123). Vector ALU arithmetic (no matrix cores): for unusual
- * dims, not for speed. Arguments mean what they mean for tmla_mla_decode;
+ * (kernel.py:123). bf16 / fp16 calls with head_dim_v <= 512 and
+ * head_dim_v + rope_dim <= 576 run on matrix cores (v_mfma_f32_16x16x32,
+ * 64 heads per workgroup), the others on the vector ALU (16 heads per
+ * workgroup): for unusual dims, not at the speed of the kernels above. Arguments mean what they mean for tmla_mla_decode;
  * num_splits in [1, 65535]; batch and num_heads at most 65535; the
  * workspace is tmla_generic_workspace_bytes(batch, num_heads, head_dim_v,
  * num_splits) bytes and needs no initialisation. Sequence lengths above the
  * cache's capacity are cut to it.
  */
 size_t tmla_generic_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v, int32_t num_splits);
+/*
+ * Heads per workgroup of tmla_mla_decode_generic's stage 1 for these dims and
+ * element type (64: the matrix-core form, for bf16 / fp16 with head_dim_v <=
+ * 512 and head_dim_v + rope_dim <= 576; 16: the vector-ALU form; 0: not
+ * accepted), for callers that size num_splits to the device. No counterpart
+ * in the reference (its autotune picks BLOCK_H, kernel.py:32-46).
+ */
+int32_t tmla_generic_heads_per_workgroup(int32_t head_dim_v, int32_t rope_dim, int32_t dtype);
 int tmla_mla_decode_generic(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
                             int64_t kv_stride_0, int64_t kv_stride_1, int64_t num_blocks, int32_t page_size,
                             const int32_t* block_table, int64_t bt_stride_b, int32_t bt_cols,

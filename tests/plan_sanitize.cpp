@@ -103,6 +103,16 @@ int main() {
           EXPECT(64 * d + kGenProbBytes + (int64_t)gp.tile * gp.pitch <= gp.lds, "LDS fits dv=%d dr=%d", dv, dr);
           EXPECT(gp.pitch % 16 == 0 && gp.pitch == d * elem_bytes(dt) + 16, "pitch");
           EXPECT(gp.lds <= 160 * 1024 && (gp.lds != kGenSmallLds || gp.tile >= 16), "the small form holds 16 rows");
+          // the matrix-core form: bf16 / fp16 at dv <= 512 and D <= 576 only, inside its LDS form, and
+          // at most 9 16-byte chunks per thread and step (32 rows of D / 8 chunks over 256 threads)
+          const int mf = generic_mfma_form(dv, dr, dt);
+          const bool mf_ok = dt != TMLA_FP32 && dv <= 512 && d <= 576;
+          EXPECT((mf != 0) == mf_ok, "mfma form applies dv=%d dr=%d dt=%d", dv, dr, dt);
+          if (mf) {
+            EXPECT(generic_mfma_lds_need(dv, dr) <= mf && mf <= 160 * 1024, "mfma LDS dv=%d dr=%d", dv, dr);
+            EXPECT(kGenMfmaTokens * (d / 8) <= 9 * 256, "mfma chunks per thread");
+            EXPECT(mf == kGenMfmaLargeLds || 2 * kGenMfmaSmallLds <= 160 * 1024, "two small forms per CU");
+          }
         }
         for (int32_t b : gbatches)
           for (int32_t h : gheads)

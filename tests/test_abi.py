@@ -144,6 +144,14 @@ def test_generic_workspace_and_rejections(lib):
     # null tensors are caught before any launch
     assert _generic(lib, ws=fake, wsb=ws) == 1
     assert b"NULL" in lib.tmla_last_error()
+    # heads per workgroup: the matrix-core form (bf16 / fp16, dv <= 512, D <= 576) or the vector-ALU one
+    assert lib.tmla_generic_heads_per_workgroup(512, 64, 0) == 64
+    assert lib.tmla_generic_heads_per_workgroup(256, 32, 1) == 64
+    assert lib.tmla_generic_heads_per_workgroup(512, 128, 0) == 16
+    assert lib.tmla_generic_heads_per_workgroup(1024, 64, 1) == 16
+    assert lib.tmla_generic_heads_per_workgroup(128, 32, 2) == 16
+    assert lib.tmla_generic_heads_per_workgroup(96, 32, 0) == 0
+    assert lib.tmla_generic_heads_per_workgroup(128, 32, 3) == 0
     # the matrix-core entry points keep refusing float32
     assert _partial(lib, dtype=2, ws=fake, wsb=lib.tmla_workspace_bytes(2, 128, 512, 1, 0)) == 1
 

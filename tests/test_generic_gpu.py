@@ -13,7 +13,10 @@ rows; out == 0 and lse == -inf exactly for empty sequences; one-token
 sequences return the cached latent row itself (bit-exact gather through the
 block table). Also: the element-load path for cache rows that do not start
 on 16-byte boundaries, split-count invariance, and the generic kernels
-against the matrix-core decode at 512 + 64 in bf16 (through the C ABI).
+against the matrix-core decode at 512 + 64 in bf16 (through the C ABI). bf16 and
+fp16 calls with head_dim_v <= 512 and D <= 576 run the generic kernels'
+matrix-core form, the others (and fp32) the vector-ALU form; the cases cover
+both forms in both 16-bit types.
 """
 
 import ctypes
@@ -70,6 +73,9 @@ CASES = [  # head_dim_v, rope_dim, dtype, heads, page size (0: dense), num_split
     (512, 16, torch.float16, 16, 16, 16),
     (1024, 64, torch.bfloat16, 16, 64, 3),
     (1024, 256, torch.float32, 16, 0, 2),
+    (1024, 16, torch.float16, 16, 16, 4),
+    (256, 32, torch.float16, 65, 64, None),
+    (64, 16, torch.bfloat16, 130, 32, 2),
 ]
 
 
@@ -113,8 +119,9 @@ def test_generic_default_scale_and_flashmla_layout(gpu):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_generic_unaligned_rows_and_split_invariance(gpu, dtype):
-    """Cache rows one element off 16-byte boundaries take the element-load
-    path; results agree with the aligned copy and across split counts."""
+    """Cache rows one element off 16-byte boundaries take the vector-ALU form's
+    element loads (bf16 aligned rows take the matrix-core form); results agree
+    with the aligned copy and across split counts."""
     import triton_mla
 
     g = torch.Generator().manual_seed(5)
@@ -130,8 +137,11 @@ def test_generic_unaligned_rows_and_split_invariance(gpu, dtype):
     b = triton_mla.mla_decode(q, kv, sl, head_dim_v=dv, num_splits=3, return_lse=True)
     c = triton_mla.mla_decode(q, kv, sl, head_dim_v=dv, num_splits=1, return_lse=True)
     torch.cuda.synchronize()
-    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
     otol, ltol = TOL[dtype]
+    if dtype == torch.float32:  # both on the vector ALU: the same bits
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    else:  # unaligned rows take the vector-ALU form, aligned ones the matrix-core form
+        torch.testing.assert_close(a[0].float(), b[0].float(), atol=otol, rtol=otol)
     torch.testing.assert_close(b[0].float(), c[0].float(), atol=otol, rtol=otol)
     _check(a[0], a[1], q.cpu(), kv.cpu(), seqlens, None, dv, d ** -0.5, dtype)
 

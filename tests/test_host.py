@@ -87,6 +87,7 @@ def test_generic_default_splits():
     assert _generic_splits(1, 16, 0, 256) == 1
     assert _generic_splits(4096, 128, 1 << 20, 256) == 1
     assert _generic_splits(1, 1, 1 << 30, 1 << 20) == 65535
+    assert _generic_splits(32, 128, 8192, 256, heads_per_wg=64) == 16  # 64 workgroup groups
 
 
 def test_torch_reference_functions_match_oracle():

@@ -222,6 +222,30 @@ inline GenericPlan generic_plan(int32_t dv, int32_t dr, int32_t dtype) {
   return p;
 }
 
+// The matrix-core form of the generic decode (bf16 / fp16, head_dim_v <= 512,
+// D = head_dim_v + rope_dim <= 576): workgroups of 4 waves x 16 heads over
+// 32-token steps. LDS: the rows (32 x (2D + 16) bytes), the value dims
+// transposed ([dv][32 tokens], 80-byte rows), the probabilities (4 waves x
+// 16 heads x 80 bytes) and Q (64 heads x (2D + 16) bytes). 0 when the form
+// does not apply; else the LDS form (kGenMfmaSmallLds: two workgroups per
+// compute unit, or kGenMfmaLargeLds).
+constexpr int kGenMfmaTokens = 32;
+constexpr int kGenMfmaHeads = 64;
+constexpr int kGenMfmaSmallLds = 78 * 1024;
+constexpr int kGenMfmaLargeLds = 156 * 1024;
+
+inline int64_t generic_mfma_lds_need(int32_t dv, int32_t dr) {
+  const int64_t d = (int64_t)dv + dr;
+  return kGenMfmaTokens * (2 * d + 16) + (int64_t)dv * 80 + 4 * 16 * 80 + kGenMfmaHeads * (2 * d + 16);
+}
+
+inline int generic_mfma_form(int32_t dv, int32_t dr, int32_t dtype) {
+  if (dtype != TMLA_BF16 && dtype != TMLA_FP16) return 0;
+  if (dv > 512 || (int64_t)dv + dr > 576) return 0;
+  const int64_t need = generic_mfma_lds_need(dv, dr);
+  return need <= kGenMfmaSmallLds ? kGenMfmaSmallLds : (need <= kGenMfmaLargeLds ? kGenMfmaLargeLds : 0);
+}
+
 // Workspace of a generic call: the float32 partial rows, then their lse
 // values (both 256-byte aligned); 0 for invalid or too large arguments.
 inline size_t generic_workspace_bytes(int32_t batch, int32_t heads, int32_t dv, int32_t splits) {

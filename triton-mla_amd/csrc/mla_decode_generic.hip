@@ -29,7 +29,11 @@
 // Stage 2 (mla_generic_combine_kernel), one wave per (sequence, head): the
 // merge of kernel.py:163-181, w = exp2(lse_s - max) in split order.
 //
-// Plain vector ALU arithmetic in float32; no matrix cores and no LDS-DMA.
+// Stage 1 above is the vector-ALU form (float32 arithmetic, any accepted dims
+// and types); bf16 / fp16 calls with head_dim_v <= 512, head_dim_v +
+// rope_dim <= 576 and 16-byte aligned q and cache rows take the matrix-core
+// form further down (mla_generic_mfma_kernel), which writes the same partial
+// format. Neither uses LDS-DMA.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -59,6 +63,7 @@ struct GenericArgs {
   int32_t tile;      // tokens per LDS step
   int32_t pitch;     // LDS bytes per staged row
   int32_t vec;       // 1: cache rows start on 16-byte boundaries
+  int32_t qvec;      // 1: q rows start on 16-byte boundaries
   float* mid_o;      // [batch, heads, splits, dv]
   float* mid_lse;    // [batch, heads, splits], base 2
   char* out;
@@ -152,10 +157,22 @@ __global__ __launch_bounds__(256) void mla_generic_partial_kernel(GenericArgs a)
   const int start = (int)min((int64_t)s * split_len, (int64_t)n);
   const int end = (int)min((int64_t)start + split_len, (int64_t)n);
 
-  for (int i = tid; i < kGenHeads * D; i += 256) {
-    const int h = i / D, d = i - h * D;
-    const int hg = hb * kGenHeads + h;
-    qs[i] = hg < a.heads ? E::ld(a.q + ((int64_t)b * a.q_sb + (int64_t)hg * a.q_sh + d) * ES) * a.qk_scale : 0.0f;
+  // Q: eight loads in flight per thread before their stores
+  for (int i0 = tid; i0 < kGenHeads * D; i0 += 8 * 256) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = i0 + 256 * k;
+      v[k] = 0.0f;
+      if (i < kGenHeads * D) {
+        const int h = i / D, d = i - h * D;
+        const int hg = hb * kGenHeads + h;
+        if (hg < a.heads) v[k] = E::ld(a.q + ((int64_t)b * a.q_sb + (int64_t)hg * a.q_sh + d) * ES);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (i0 + 256 * k < kGenHeads * D) qs[i0 + 256 * k] = v[k] * a.qk_scale;
   }
 
   // scores: token t_qk, dim groups c_qk, c_qk + C, ... of 8
@@ -325,6 +342,252 @@ __global__ __launch_bounds__(64) void mla_generic_combine_kernel(GenericArgs a) 
   if (a.lse != nullptr && lane == 0) a.lse[row] = w_sum > 0.0f ? (m + log2f(w_sum)) * kLn2 : -INFINITY;
 }
 
+
+// ---------------------------------------------------------------------------
+// Matrix-core form (bf16 / fp16, head_dim_v <= 512, D <= 576)
+// ---------------------------------------------------------------------------
+//
+// The same algorithm and partial format on v_mfma_f32_16x16x32: a workgroup
+// of 4 waves takes 64 heads (16 per wave) and steps over 32 tokens:
+//   * the 32 cache rows are loaded into registers one step ahead (16 bytes
+//     per lane and chunk) and written to LDS twice: as rows (the S operand)
+//     and, for the value dims, transposed to [dim][token] (the PV operand);
+//   * S (16 heads x 16 tokens, two tiles) = Q . K^T over k-chunks of 32 dims:
+//     lane l reads 8 consecutive dims 32c + 8(l/16) of head l%16 (Q) and of
+//     token l%16 (K), the same k order for both operands; a last chunk of 16
+//     dims gives its upper lane groups zeros. Result: lane l holds token
+//     l%16, heads 4(l/16) + i;
+//   * the online softmax per head reduces over the 16 lanes of a group;
+//     probabilities rounded to the element type go through LDS to the layout
+//     of the PV operand (head l%16, tokens 8(l/16)..+7);
+//   * O (16 heads x 16 dims per tile) += P . V, dims 16n + l%16 from the
+//     transposed values; lane l holds dim 16n + l%16 of heads 4(l/16) + i,
+//     the heads of the softmax state it holds, so the rescale stays in-lane.
+constexpr int kMP = 2 * kGenMfmaTokens + 16;  // bytes per row of the transposed values and probabilities
+
+// Workgroup barrier after this wave's LDS accesses have completed, without
+// waiting for its global loads (a __syncthreads would also wait for the
+// next step's row loads, which are meant to fly across the barrier).
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(const i16x8& a, const i16x8& b, const f32x4& c) {
+  if constexpr (DT == TMLA_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                    0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                   0, 0);
+}
+
+// Reductions over the 16 lanes of a DPP row (lanes 16r .. 16r + 15): row
+// rotations by 8, 4, 2 and 1 leave every lane with the row's result.
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x120 | N, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float group16_max(float x) {
+  x = fmaxf(x, row_ror<8>(x));
+  x = fmaxf(x, row_ror<4>(x));
+  x = fmaxf(x, row_ror<2>(x));
+  return fmaxf(x, row_ror<1>(x));
+}
+__device__ __forceinline__ float group16_sum(float x) {
+  x += row_ror<8>(x);
+  x += row_ror<4>(x);
+  x += row_ror<2>(x);
+  return x + row_ror<1>(x);
+}
+
+// NDT: 16-dim output tiles (head_dim_v / 16)
+template <int DT, int LDSB, int NDT>
+__global__ __launch_bounds__(256) void mla_generic_mfma_kernel(GenericArgs a) {
+  using E = GElt<DT>;
+  constexpr int MT = kGenMfmaTokens;
+  constexpr int kPreU = 3;  // units (4 rows x 16 bytes) per thread and step: 8 x 576 / 8 / 256 <= 3
+  static_assert(NDT >= 1 && NDT <= 32, "head_dim_v <= 512");
+  __shared__ __attribute__((aligned(16))) char smem[LDSB];
+  const int hb = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int D = a.dv + a.dr, DV = a.dv;
+  const int rp = 2 * D + 16;  // bytes per staged row (and per Q row)
+  char* const R = smem;                        // [32 tokens][rp]
+  char* const VT = R + MT * rp;                // [DV][kMP]
+  char* const Pw = VT + DV * kMP + wave * 16 * kMP;    // [16 heads][kMP] of this wave
+  char* const Qw = VT + DV * kMP + 4 * 16 * kMP + wave * 16 * rp;  // [16 heads][rp] of this wave
+
+  const int n = (int)min(min((int64_t)max(a.seqlens[b], 0), a.capacity), (int64_t)INT32_MAX - 128);
+  const int split_len = (int)(((int64_t)n + a.splits - 1) / a.splits);
+  const int start = (int)min((int64_t)s * split_len, (int64_t)n);
+  const int end = (int)min((int64_t)start + split_len, (int64_t)n);
+
+  // Q rows of the wave's 16 heads in 16-byte chunks, eight in flight per lane
+  const int qn = 16 * (D / 8);
+  for (int i0 = lane; i0 < qn; i0 += 8 * 64) {
+    i16x8 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = i0 + 64 * k;
+      v[k] = (i16x8)0;
+      if (i < qn) {
+        const int r = i / (D / 8), ch = i - r * (D / 8);
+        const int hg = hb * kGenMfmaHeads + wave * 16 + r;
+        if (hg < a.heads) v[k] = *(const i16x8*)(a.q + ((int64_t)b * a.q_sb + (int64_t)hg * a.q_sh + ch * 8) * 2);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = i0 + 64 * k;
+      if (i < qn) {
+        const int r = i / (D / 8), ch = i - r * (D / 8);
+        *(i16x8*)(Qw + r * rp + ch * 16) = v[k];
+      }
+    }
+  }
+
+  const int g = lane >> 4, c16 = lane & 15;
+  const int nkc = (D + 31) / 32;
+  const bool half_last = (D & 31) != 0;
+  const int cpr = D / 8;      // 16-byte chunks per row
+  const int vcpr = DV / 8;    // ... of which hold value dims
+  const int nun = (MT / 4) * cpr;  // units of 4 rows x one chunk
+
+  f32x4 acc[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) acc[t] = (f32x4)0.0f;
+  float m_run[4], l_run[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.0f;
+  }
+
+  // unit u: rows 4(u % 8) .. +3, 16-byte column u / 8; the transposed
+  // values take one 8-byte write (4 tokens) per value dim of the unit, and
+  // the 8 lanes of one column fill 64 contiguous bytes of a transposed row
+  // Straight-line loads (rows past the piece read its last row and are
+  // zeroed afterwards), so all of a step's page ids, then all of its rows,
+  // are in flight together. The form is used only for 16-byte aligned rows.
+  f32x4 pre[4 * kPreU];
+  auto fetch = [&](int n0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < kPreU; ++k) {
+      const int u = tid + 256 * k;
+      if (u < nun) {
+        const int t4 = u & 7, ch = u >> 3;
+        const char* src[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) src[r] = row_ptr(a, b, min(n0 + 4 * t4 + r, end - 1), 2) + ch * 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pre[4 * k + r] = *(const f32x4*)src[r];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n0 + 4 * t4 + r >= end) pre[4 * k + r] = (f32x4)0.0f;
+      }
+    }
+  };
+  auto store = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < kPreU; ++k) {
+      const int u = tid + 256 * k;
+      if (u < nun) {
+        const int t4 = u & 7, ch = u >> 3;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) *(f32x4*)(R + (4 * t4 + r) * rp + ch * 16) = pre[4 * k + r];
+        if (ch < vcpr) {
+          const i16x8 v0 = __builtin_bit_cast(i16x8, pre[4 * k]), v1 = __builtin_bit_cast(i16x8, pre[4 * k + 1]);
+          const i16x8 v2 = __builtin_bit_cast(i16x8, pre[4 * k + 2]), v3 = __builtin_bit_cast(i16x8, pre[4 * k + 3]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const i16x4 col = {v0[e], v1[e], v2[e], v3[e]};
+            *(i16x4*)(VT + (ch * 8 + e) * kMP + 8 * t4) = col;
+          }
+        }
+      }
+    }
+  };
+
+  if (start < end) fetch(start);
+  for (int n0 = start; n0 < end; n0 += MT) {
+    lds_sync();  // Q staged; the previous step's operands read
+    store();
+    lds_sync();
+    if (n0 + MT < end) fetch(n0 + MT);  // in flight until the next store
+
+    // S, the operands of chunk c + 1 read before the MFMAs of chunk c
+    f32x4 s0 = (f32x4)0.0f, s1 = (f32x4)0.0f;
+    auto operands = [&](int c, i16x8& qa, i16x8& k0, i16x8& k1) __attribute__((always_inline)) {
+      qa = (i16x8)0;
+      k0 = (i16x8)0;
+      k1 = (i16x8)0;
+      if (!(half_last && c == nkc - 1 && g >= 2)) {
+        const int off = (32 * c + 8 * g) * 2;
+        qa = *(const i16x8*)(Qw + c16 * rp + off);
+        k0 = *(const i16x8*)(R + c16 * rp + off);
+        k1 = *(const i16x8*)(R + (16 + c16) * rp + off);
+      }
+    };
+    i16x8 qa, k0, k1;
+    operands(0, qa, k0, k1);
+    for (int c = 0; c < nkc; ++c) {
+      i16x8 qn = qa, kn0 = k0, kn1 = k1;
+      if (c + 1 < nkc) operands(c + 1, qn, kn0, kn1);
+      s0 = mfma16<DT>(qa, k0, s0);
+      s1 = mfma16<DT>(qa, k1, s1);
+      qa = qn;
+      k0 = kn0;
+      k1 = kn1;
+    }
+
+    const bool v0 = n0 + c16 < end, v1 = n0 + 16 + c16 < end;
+    float alpha[4];
+    bool moved = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x0 = v0 ? s0[i] * a.qk_scale : -INFINITY;
+      const float x1 = v1 ? s1[i] * a.qk_scale : -INFINITY;
+      const float m_new = fmaxf(m_run[i], group16_max(fmaxf(x0, x1)));
+      alpha[i] = exp2f(m_run[i] - m_new);
+      moved |= m_new != m_run[i];
+      const float e0 = v0 ? exp2f(x0 - m_new) : 0.0f;
+      const float e1 = v1 ? exp2f(x1 - m_new) : 0.0f;
+      l_run[i] = l_run[i] * alpha[i] + group16_sum(e0 + e1);
+      m_run[i] = m_new;
+      *(short*)(Pw + (4 * g + i) * kMP + c16 * 2) = Elt<DT>::from_float(e0);
+      *(short*)(Pw + (4 * g + i) * kMP + (16 + c16) * 2) = Elt<DT>::from_float(e1);
+    }
+    // a head whose max did not move has alpha = 1 exactly, so the rescale is
+    // skipped when no head of the wave moved (the same bits)
+    if (__any(moved)) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] *= alpha[i];
+    }
+    lds_sync();
+
+    const i16x8 pa = *(const i16x8*)(Pw + c16 * kMP + 16 * g);
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      const i16x8 vb = *(const i16x8*)(VT + (16 * t + c16) * kMP + 16 * g);
+      acc[t] = mfma16<DT>(pa, vb, acc[t]);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int hg = hb * kGenMfmaHeads + wave * 16 + 4 * g + i;
+    if (hg >= a.heads) continue;
+    const bool has = l_run[i] > 0.0f;
+    const float den = has ? l_run[i] : 1.0f;
+    const int64_t row = ((int64_t)b * a.heads + hg) * a.splits + s;
+    float* dst = a.mid_o + row * DV;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) dst[16 * t + c16] = acc[t][i] / den;
+    if (c16 == 0) a.mid_lse[row] = has ? m_run[i] + log2f(l_run[i]) : -INFINITY;
+  }
+}
+
 template <int DT, int NGL>
 hipError_t launch_partial_t(const GenericArgs& a, int lds, dim3 grid, hipStream_t stream) {
   if (lds == kGenSmallLds)
@@ -334,11 +597,43 @@ hipError_t launch_partial_t(const GenericArgs& a, int lds, dim3 grid, hipStream_
   return hipGetLastError();
 }
 
+template <int DT, int NDT>
+hipError_t launch_mfma_ndt(const GenericArgs& a, int lds, dim3 grid, hipStream_t stream) {
+  if (lds == kGenMfmaSmallLds)
+    hipLaunchKernelGGL((mla_generic_mfma_kernel<DT, kGenMfmaSmallLds, NDT>), grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((mla_generic_mfma_kernel<DT, kGenMfmaLargeLds, NDT>), grid, dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
 template <int DT>
-hipError_t launch_t(const GenericArgs& a, int lds, hipStream_t stream) {
+hipError_t launch_mfma_t(const GenericArgs& a, int lds, hipStream_t stream) {
+  const dim3 grid((a.heads + kGenMfmaHeads - 1) / kGenMfmaHeads, a.splits, a.batch);
+  switch (a.dv) {
+    case 16: return launch_mfma_ndt<DT, 1>(a, lds, grid, stream);
+    case 32: return launch_mfma_ndt<DT, 2>(a, lds, grid, stream);
+    case 64: return launch_mfma_ndt<DT, 4>(a, lds, grid, stream);
+    case 128: return launch_mfma_ndt<DT, 8>(a, lds, grid, stream);
+    case 256: return launch_mfma_ndt<DT, 16>(a, lds, grid, stream);
+    default: return launch_mfma_ndt<DT, 32>(a, lds, grid, stream);  // 512 (generic_mfma_form: dv <= 512)
+  }
+}
+
+// lds: the vector-ALU form's LDS; mfma_lds: the matrix-core form's, or 0
+// when that form does not apply.
+template <int DT>
+hipError_t launch_t(const GenericArgs& a, int lds, int mfma_lds, hipStream_t stream) {
+  hipError_t e;
+  if constexpr (DT != TMLA_FP32) {
+    if (mfma_lds != 0) {
+      e = launch_mfma_t<DT>(a, mfma_lds, stream);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((mla_generic_combine_kernel<DT>), dim3(a.batch, a.heads), dim3(64), 0, stream, a);
+      return hipGetLastError();
+    }
+  }
   const dim3 grid((a.heads + kGenHeads - 1) / kGenHeads, a.splits, a.batch);
-  const hipError_t e = a.dv == 1024 ? launch_partial_t<DT, 2>(a, lds, grid, stream)
-                                    : launch_partial_t<DT, 1>(a, lds, grid, stream);
+  e = a.dv == 1024 ? launch_partial_t<DT, 2>(a, lds, grid, stream) : launch_partial_t<DT, 1>(a, lds, grid, stream);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((mla_generic_combine_kernel<DT>), dim3(a.batch, a.heads), dim3(64), 0, stream, a);
   return hipGetLastError();
@@ -356,6 +651,12 @@ extern "C" {
 
 size_t tmla_generic_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim_v, int32_t num_splits) {
   return generic_workspace_bytes(batch, num_heads, head_dim_v, num_splits);
+}
+
+int32_t tmla_generic_heads_per_workgroup(int32_t head_dim_v, int32_t rope_dim, int32_t dtype) {
+  if (dtype != TMLA_BF16 && dtype != TMLA_FP16 && dtype != TMLA_FP32) return 0;
+  if (!pow2_between(head_dim_v, 16, 1024) || !pow2_between(rope_dim, 16, 256)) return 0;
+  return generic_mfma_form(head_dim_v, rope_dim, dtype) != 0 ? kGenMfmaHeads : kGenHeads;
 }
 
 int tmla_mla_decode_generic(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kv,
@@ -399,6 +700,7 @@ int tmla_mla_decode_generic(const void* q, int64_t q_stride_b, int64_t q_stride_
   a.tile = p.tile;
   a.pitch = p.pitch;
   a.vec = ((uintptr_t)kv % 16 == 0 && (kv_stride_0 * es) % 16 == 0 && (kv_stride_1 * es) % 16 == 0) ? 1 : 0;
+  a.qvec = ((uintptr_t)q % 16 == 0 && (q_stride_b * es) % 16 == 0 && (q_stride_h * es) % 16 == 0) ? 1 : 0;
   const int64_t rows = (int64_t)batch * num_heads * num_splits;
   a.mid_o = (float*)workspace;
   a.mid_lse = (float*)((char*)workspace + ((rows * head_dim_v * 4 + 255) & ~(int64_t)255));
@@ -407,9 +709,11 @@ int tmla_mla_decode_generic(const void* q, int64_t q_stride_b, int64_t q_stride_
   a.out_sh = out_stride_h;
   a.lse = lse;
   hipStream_t st = (hipStream_t)stream;
-  const hipError_t e = dtype == TMLA_BF16   ? gen::launch_t<TMLA_BF16>(a, p.lds, st)
-                       : dtype == TMLA_FP16 ? gen::launch_t<TMLA_FP16>(a, p.lds, st)
-                                            : gen::launch_t<TMLA_FP32>(a, p.lds, st);
+  // the matrix-core form reads q and the cache in 16-byte pieces only
+  const int mfma_lds = a.vec && a.qvec ? generic_mfma_form(head_dim_v, rope_dim, dtype) : 0;
+  const hipError_t e = dtype == TMLA_BF16   ? gen::launch_t<TMLA_BF16>(a, p.lds, mfma_lds, st)
+                       : dtype == TMLA_FP16 ? gen::launch_t<TMLA_FP16>(a, p.lds, mfma_lds, st)
+                                            : gen::launch_t<TMLA_FP32>(a, p.lds, mfma_lds, st);
   return e == hipSuccess ? TMLA_OK : hip_fail(e, "mla_generic kernels launch");
 }
 

@@ -55,6 +55,7 @@ SIGNATURES = {
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _i32, _i32,
         _i32, _i32, _i32, _f32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "tmla_generic_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
+    "tmla_generic_heads_per_workgroup": (_i32, [_i32, _i32, _i32]),
     "tmla_mla_decode_generic": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _f32,
         _i32, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),

@@ -439,11 +439,12 @@ def mla_decode(
 _GENERIC_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
-def _generic_splits(batch, num_heads, capacity, num_sms):
-    """Default split count of the generic decode: about four workgroups (16
-    heads, one piece of a sequence) per compute unit, pieces of at least 256
-    tokens of the cache's capacity, at most 65535 (the launch's grid.y)."""
-    groups = max(batch * -(-num_heads // 16), 1)
+def _generic_splits(batch, num_heads, capacity, num_sms, heads_per_wg=16):
+    """Default split count of the generic decode: about four workgroups
+    (heads_per_wg heads, one piece of a sequence) per compute unit, pieces of
+    at least 256 tokens of the cache's capacity, at most 65535 (the launch's
+    grid.y)."""
+    groups = max(batch * -(-num_heads // heads_per_wg), 1)
     by_cus = -(-4 * num_sms // groups)
     by_len = max(-(-capacity // 256), 1)
     return max(1, min(by_cus, by_len, 65535))
@@ -456,9 +457,10 @@ def _generic_decode(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax
     reference's kernels take powers of two and any dtype q and the cache
     share (kernel.py:243-245). Both of the reference's stages with its
     uniform splits (kernel.py:84-86) and float32 partials; ``num_splits=None``
-    takes _generic_splits of the cache's capacity (sized for this kernel's
-    16-head workgroups; no call reads ``cache_seqlens`` back to the host).
-    Vector ALU kernels: meant for unusual dims, not for speed."""
+    takes _generic_splits of the cache's capacity (sized for the form's
+    workgroups: 64 heads on matrix cores for bf16 / fp16 up to 512 + 64, 16
+    on the vector ALU otherwise; no call reads ``cache_seqlens`` back to the
+    host). Meant for unusual dims, not at the 512 + 64 kernels' speed."""
     # validation mirrors kernel.py:235-245
     if kv_cache.dim() == 4:
         assert kv_cache.shape[2] == 1, "MLA uses a single shared latent KV head"
@@ -500,7 +502,8 @@ def _generic_decode(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax
         capacity = num_blocks
         bt_args = (None, 0, 1)
     if num_splits is None:
-        num_splits = _generic_splits(batch, num_heads, capacity, _num_sms(device))
+        per_wg = _native.load().tmla_generic_heads_per_workgroup(head_dim_v, d_rope, _native.DTYPE_CODE[q.dtype])
+        num_splits = _generic_splits(batch, num_heads, capacity, _num_sms(device), max(per_wg, 1))
     num_splits = int(num_splits)
     assert num_splits >= 1, "num_splits must be >= 1"
     out = torch.empty(batch, num_heads, head_dim_v, dtype=q.dtype, device=device)
