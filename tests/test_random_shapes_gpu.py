@@ -8,7 +8,8 @@ the single launch or two kernels. Each call is checked at the parity bar
 (out atol = rtol = 1e-2, lse 1e-3 on non-empty rows, empty sequences exactly
 0 and -inf) and against the other launch form bit for bit. The same draws
 also run over an fp8 cache (against the fp8 oracle) and with 1-8 query
-tokens per sequence (against the causal oracle).
+tokens per sequence (against the causal oracle), and at other power-of-two
+head dims and fp32 (the generic decode).
 """
 
 import numpy as np
@@ -154,3 +155,48 @@ def test_random_shape_multi_token(gpu, seed):
     seen = seen[:, :, None].expand(batch, q_len, heads)
     torch.testing.assert_close(lse[seen], torch.from_numpy(ref_lse)[seen], atol=1e-3, rtol=1e-3)
     assert torch.all(out[~seen] == 0) and torch.all(torch.isneginf(lse[~seen]))
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_shape_other_dims(gpu, seed):
+    """Other head dims and fp32 (the generic decode, both of its forms): the
+    same draws of batch, heads, lengths, paging and splits at random
+    power-of-two dims, against the float64 oracle (fp32 at 1e-4)."""
+    import triton_mla
+
+    batch, heads, max_len, lens, page, splits, dtype = _draw(1300 + seed)
+    rng = np.random.default_rng(1700 + seed)
+    dv = int(rng.choice([16, 32, 64, 128, 256, 512, 1024]))
+    dr = int(rng.choice([16, 32, 64, 128, 256]))
+    if (dv, dr) == (512, 64) or seed % 4 == 0:
+        dtype = torch.float32
+    d = dv + dr
+    name = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype]
+    print(f"generic seed {seed}: batch={batch} heads={heads} max_len={max_len} page={page} splits={splits} "
+          f"dims {dv}+{dr} {name}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, heads, d, generator=g).to(dtype)
+    kv = torch.randn(batch, max_len, d, generator=g).to(dtype)
+    bt = None
+    if page:
+        per_seq = -(-max_len // page) + 1
+        blocks = batch * per_seq
+        bt = torch.randperm(blocks, generator=g).view(batch, per_seq).int()
+        padded = torch.zeros(batch, per_seq * page, d, dtype=dtype)
+        padded[:, :max_len] = kv
+        kv = torch.empty(blocks, page, d, dtype=dtype)
+        kv[bt.long()] = padded.view(batch, per_seq, page, d)
+    sm = d ** -0.5
+    out, lse = triton_mla.mla_decode(q.to(gpu), kv.to(gpu), torch.from_numpy(lens).to(gpu),
+                                     None if bt is None else bt.to(gpu), head_dim_v=dv, softmax_scale=sm,
+                                     num_splits=splits, return_lse=True)
+    torch.cuda.synchronize()
+    as_o = (lambda t: t.contiguous().numpy()) if dtype == torch.float32 else bits
+    ref_out, ref_lse = oracle.mla_decode_ref(as_o(q), as_o(kv), lens, None if bt is None else bt.numpy(), dv, sm,
+                                             dtype=name)
+    otol, ltol = (1e-4, 1e-4) if dtype == torch.float32 else (1e-2, 1e-3)
+    out, lse = out.float().cpu(), lse.cpu()
+    torch.testing.assert_close(out, torch.from_numpy(ref_out), atol=otol, rtol=otol)
+    valid = torch.from_numpy(lens > 0)
+    torch.testing.assert_close(lse[valid], torch.from_numpy(ref_lse)[valid], atol=ltol, rtol=ltol)
+    assert torch.all(out[~valid] == 0) and torch.all(torch.isneginf(lse[~valid]))
