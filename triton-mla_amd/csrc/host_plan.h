@@ -226,17 +226,28 @@ inline GenericPlan generic_plan(int32_t dv, int32_t dr, int32_t dtype) {
 // D = head_dim_v + rope_dim <= 576): workgroups of 4 waves x 16 heads over
 // 32-token steps. LDS: the rows (32 x (2D + 16) bytes), the value dims
 // transposed ([dv][32 tokens], 80-byte rows), the probabilities (4 waves x
-// 16 heads x 80 bytes) and Q (64 heads x (2D + 16) bytes). 0 when the form
+// 16 heads x 80 bytes) and Q (64 heads x (2D + 16) bytes) (the 16-byte
+// paddings are kGenRowPad and kGenMP - 64). 0 when the form
 // does not apply; else the LDS form (kGenMfmaSmallLds: two workgroups per
 // compute unit, or kGenMfmaLargeLds).
 constexpr int kGenMfmaTokens = 32;
 constexpr int kGenMfmaHeads = 64;
+// padding bytes of the staged rows and of the transposed rows (bank spread)
+#ifndef TMLA_GEN_ROW_PAD
+#define TMLA_GEN_ROW_PAD 16
+#endif
+#ifndef TMLA_GEN_MP_PAD
+#define TMLA_GEN_MP_PAD 16
+#endif
+constexpr int kGenRowPad = TMLA_GEN_ROW_PAD;
+constexpr int kGenMP = 2 * kGenMfmaTokens + TMLA_GEN_MP_PAD;
 constexpr int kGenMfmaSmallLds = 78 * 1024;
 constexpr int kGenMfmaLargeLds = 156 * 1024;
 
 inline int64_t generic_mfma_lds_need(int32_t dv, int32_t dr) {
   const int64_t d = (int64_t)dv + dr;
-  return kGenMfmaTokens * (2 * d + 16) + (int64_t)dv * 80 + 4 * 16 * 80 + kGenMfmaHeads * (2 * d + 16);
+  return kGenMfmaTokens * (2 * d + kGenRowPad) + (int64_t)dv * kGenMP + 4 * 16 * kGenMP +
+         kGenMfmaHeads * (2 * d + kGenRowPad);
 }
 
 inline int generic_mfma_form(int32_t dv, int32_t dr, int32_t dtype) {

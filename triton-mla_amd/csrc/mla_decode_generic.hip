@@ -363,7 +363,7 @@ __global__ __launch_bounds__(64) void mla_generic_combine_kernel(GenericArgs a) 
 //   * O (16 heads x 16 dims per tile) += P . V, dims 16n + l%16 from the
 //     transposed values; lane l holds dim 16n + l%16 of heads 4(l/16) + i,
 //     the heads of the softmax state it holds, so the rescale stays in-lane.
-constexpr int kMP = 2 * kGenMfmaTokens + 16;  // bytes per row of the transposed values and probabilities
+constexpr int kMP = kGenMP;  // bytes per row of the transposed values and probabilities
 
 // Workgroup barrier after this wave's LDS accesses have completed, without
 // waiting for its global loads (a __syncthreads would also wait for the
@@ -410,7 +410,7 @@ __global__ __launch_bounds__(256) void mla_generic_mfma_kernel(GenericArgs a) {
   const int hb = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int D = a.dv + a.dr, DV = a.dv;
-  const int rp = 2 * D + 16;  // bytes per staged row (and per Q row)
+  const int rp = 2 * D + kGenRowPad;  // bytes per staged row (and per Q row)
   char* const R = smem;                        // [32 tokens][rp]
   char* const VT = R + MT * rp;                // [DV][kMP]
   char* const Pw = VT + DV * kMP + wave * 16 * kMP;    // [16 heads][kMP] of this wave
