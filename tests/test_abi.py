@@ -156,6 +156,33 @@ def test_generic_workspace_and_rejections(lib):
     assert _partial(lib, dtype=2, ws=fake, wsb=lib.tmla_workspace_bytes(2, 128, 512, 1, 0)) == 1
 
 
+def test_fast_module_carries_the_plan(lib):
+    """The CPython entry of the kept-shape call (csrc/fastcall.c) packs the
+    constant arguments once and passes them with the call's pointers to the
+    same library instance (its error text is the library's)."""
+    from triton_mla import _native
+
+    fast = _native.fast_module()
+    assert fast is not None, "build the library with triton-mla_amd/build.py (it builds the module too)"
+    fake = 1 << 20  # never dereferenced: validation fails first
+    ws = lib.tmla_workspace_bytes(2, 128, 512, 1, 0)
+
+    def plan(dtype=0, dv=512, ws_bytes=ws, splits=1):
+        return fast.plan(576 * 128, 576, 64 * 576, 576, 4, 64, 1, 1, 2, 128, dv, 64, dtype, 0.1, splits, 0,
+                         128 * 512, 512, ws_bytes)
+
+    assert fast.decode(plan(dtype=7), fake, fake, None, fake, fake, None, fake, 0) == 1
+    assert b"dtype" in lib.tmla_last_error()
+    assert fast.decode(plan(dv=256), fake, fake, None, fake, fake, None, fake, 0) == 2
+    assert fast.decode(plan(ws_bytes=ws - 1), fake, fake, None, fake, fake, None, fake, 0) == 3
+    assert fast.decode(plan(splits=0), fake, fake, None, fake, fake, None, fake, 0) == 1  # balanced needs workers
+    assert fast.decode(plan(), None, fake, None, fake, fake, None, fake, 0) == 1  # a null q is refused
+    with pytest.raises(TypeError):
+        fast.decode(plan(), fake)
+    with pytest.raises(ValueError):
+        fast.decode(object(), fake, fake, None, fake, fake, None, fake, 0)
+
+
 def test_layer_glue_arguments_rejected_on_host(lib):
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
     # tmla_mla_absorb_q(q_proj, q_sb, wkv_b, w_s0, positions, batch, heads, nope, rope, rank, vd, theta,

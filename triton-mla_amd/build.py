@@ -28,6 +28,7 @@ import re
 import shutil
 import subprocess
 import sys
+import sysconfig
 import tempfile
 from concurrent.futures import ThreadPoolExecutor
 
@@ -36,6 +37,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "triton_mla", "libtriton_mla_hip.so")
+FAST_EXT = os.path.join(HERE, "triton_mla", "_tmla_fast" + sysconfig.get_config_var("EXT_SUFFIX"))
 LIB_STAMPS = os.path.join(HERE, "triton_mla", "libtriton_mla_hip_stamps.so")
 SOURCES = ["mla_decode.hip", "mla_decode_fp8.hip", "mla_decode_g16.hip", "mla_decode_generic.hip", "mla_layer.hip"]
 ARCH = os.environ.get("TRITON_MLA_ARCH", "gfx950")
@@ -115,10 +117,27 @@ def build(verbose: bool = False, stamps: bool = False) -> str:
             raise RuntimeError(f"link failed ({res.returncode})")
     check_kernel_stubs(out + ".tmp")
     os.replace(out + ".tmp", out)
+    if not stamps:
+        build_fast_ext()
     if verbose:
         print(f"{len(usage)} kernels checked" + ("" if stamps else ", none beyond their scratch allowance") +
               ", no early MFMA result reads", flush=True)
     return out
+
+
+def build_fast_ext() -> str:
+    """The CPython module of the public call's kept-shape path (csrc/fastcall.c),
+    linked against LIB in the same directory."""
+    inc = sysconfig.get_paths()["include"]
+    cmd = [os.environ.get("CC", "gcc"), "-O2", "-shared", "-fPIC", "-Wall", f"-I{inc}", f"-I{INCLUDE}",
+           os.path.join(CSRC, "fastcall.c"), "-o", FAST_EXT + ".tmp", f"-L{os.path.dirname(LIB)}",
+           "-l:" + os.path.basename(LIB), "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"fastcall.c failed ({res.returncode})")
+    os.replace(FAST_EXT + ".tmp", FAST_EXT)
+    return FAST_EXT
 
 
 def parse_resource_usage(remarks: str) -> dict[str, dict[str, int]]:

@@ -130,6 +130,27 @@ def load_gil_held():
     return _held
 
 
+_fast = False  # not looked up yet
+
+
+def fast_module():
+    """The CPython module of the kept-shape call (csrc/fastcall.c, built beside
+    the library and linked to it), or None when it is not built or another
+    library build is selected (TRITON_MLA_LIB): callers then use the ctypes
+    binding of the same library."""
+    global _fast
+    if _fast is False:
+        mod = None
+        if not os.environ.get("TRITON_MLA_LIB"):
+            load()  # the library first, by the path the module's rpath resolves to
+            try:
+                from . import _tmla_fast as mod  # noqa: F811
+            except ImportError:
+                mod = None
+        _fast = mod
+    return _fast
+
+
 def check(status: int, what: str) -> None:
     if status != 0:
         msg = load().tmla_last_error().decode(errors="replace")

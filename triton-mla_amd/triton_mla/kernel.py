@@ -535,7 +535,7 @@ class _CallShape:
     later calls of the same shape only read addresses and allocate."""
 
     __slots__ = ("dev_idx", "device", "dtype", "out_shape", "lse_shape", "ws_alloc", "ws_bytes",
-                 "a_q", "a_kv", "a_bt", "a_mid", "a_out", "fn")
+                 "a_q", "a_kv", "a_bt", "a_mid", "a_out", "fn", "fast", "plan")
 
 
 _SHAPES = {}
@@ -594,9 +594,14 @@ def _fast_call(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scal
     lse = q.new_empty(shape.lse_shape, dtype=torch.float32) if want_lse else None
     stream = _raw_stream(shape.dev_idx)
     ws = _workspace(shape, stream)
-    status = shape.fn(qp, *shape.a_q, kp, *shape.a_kv, None if block_table is None else block_table.data_ptr(),
-                      *shape.a_bt, cache_seqlens.data_ptr(), *shape.a_mid, out.data_ptr(), *shape.a_out,
-                      None if lse is None else lse.data_ptr(), ws.data_ptr(), shape.ws_bytes, stream)
+    btp = None if block_table is None else block_table.data_ptr()
+    lsep = None if lse is None else lse.data_ptr()
+    if shape.fast is not None:
+        status = shape.fast.decode(shape.plan, qp, kp, btp, cache_seqlens.data_ptr(), out.data_ptr(), lsep,
+                                   ws.data_ptr(), stream)
+    else:
+        status = shape.fn(qp, *shape.a_q, kp, *shape.a_kv, btp, *shape.a_bt, cache_seqlens.data_ptr(), *shape.a_mid,
+                          out.data_ptr(), *shape.a_out, lsep, ws.data_ptr(), shape.ws_bytes, stream)
     if status:
         _native.check(status, "tmla_mla_decode")
     return out, lse
@@ -635,4 +640,10 @@ def _shape_of(call, dtype):
     shape.a_q, shape.a_kv, shape.a_bt = a[1:3], a[4:8], a[9:11]
     shape.a_mid, shape.a_out = a[12:20], a[21:23]
     shape.fn = _native.load_gil_held().tmla_mla_decode
+    # the same constant arguments packed once for the CPython entry
+    shape.fast = _native.fast_module()
+    shape.plan = None
+    if shape.fast is not None:
+        shape.plan = shape.fast.plan(*shape.a_q, *shape.a_kv, *shape.a_bt, *shape.a_mid, *shape.a_out,
+                                     shape.ws_bytes)
     return shape
