@@ -322,7 +322,30 @@ __global__ __launch_bounds__(64) void mla_generic_combine_kernel(GenericArgs a) 
 #pragma unroll
   for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
   float w_sum = 0.0f;
-  for (int s = 0; s < a.splits; ++s) {
+  // four splits' rows in flight at a time, merged in split order
+  int s = 0;
+  for (; s + 4 <= a.splits; s += 4) {
+    float lv[4], x[4][16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lv[j] = ml[s + j];
+      const float* src = mo + (int64_t)(s + j) * a.dv;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int d = lane + 64 * k;
+        x[j][k] = d < a.dv ? src[d] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float w = exp2f(lv[j] - m);
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (lane + 64 * k < a.dv) acc[k] = fmaf(w, x[j][k], acc[k]);
+      w_sum += w;
+    }
+  }
+  for (; s < a.splits; ++s) {
     const float w = exp2f(ml[s] - m);
     const float* src = mo + (int64_t)s * a.dv;
 #pragma unroll
