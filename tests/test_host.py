@@ -77,6 +77,23 @@ def test_other_dims_and_fp32_take_the_generic_path():
         mla_decode(q.unsqueeze(1), kv, lens, head_dim_v=128)
 
 
+def test_make_inputs_takes_the_reference_dims():
+    """make_inputs keeps the reference's arguments (bench.py:20: ..., device,
+    d_latent=512, d_rope=64) and draws the default dims exactly as before."""
+    import inspect
+
+    from triton_mla import bench, workloads
+
+    params = list(inspect.signature(bench.make_inputs).parameters)
+    assert params[:8] == ["batch", "seqlen", "num_heads", "page_size", "dtype", "device", "d_latent", "d_rope"]
+    a = bench.make_inputs(2, 100, 4, 64, torch.float32, "cpu", 128, 32)
+    assert a.q.shape == (2, 4, 160) and a.kv_cache.shape == (4, 64, 160) and a.head_dim_v == 128
+    assert a.softmax_scale == 160 ** -0.5
+    b = bench.make_inputs(2, 100, 4, 64, torch.bfloat16, "cpu")
+    c = workloads.uniform(2, 4, 100)
+    assert torch.equal(b.q, c.q) and torch.equal(b.kv_cache, c.kv_cache) and b.softmax_scale == 192 ** -0.5
+
+
 def test_generic_default_splits():
     """About four 16-head workgroups per compute unit, pieces of >= 256 tokens."""
     from triton_mla.kernel import _generic_splits

@@ -10,6 +10,8 @@ column keeps its name for drop-in CSV consumers and holds the HIP kernels'
 time; ``config`` names the launch shape that ran. Additions: --workload runs
 the named seeded workloads of triton_mla.workloads (uniform and ragged
 lengths), --splits picks the split scheme, --no-compile skips torch.compile,
+--head-dim-v / --rope-dim set the head dims (make_inputs' d_latent / d_rope:
+other dims run the generic decode), --dtype fp32 decodes float32 inputs,
 --kv-fp8 decodes an E4M3 copy of the cache, --layer times one decode step of the whole MLA layer at DeepSeek-V3 dims
 (random N(0, 0.02) bf16 weights, --batch sequences of --seqlen cached tokens)
 with the HIP glue (MLA.forward) and with the reference's torch glue
@@ -30,13 +32,14 @@ import os
 
 import torch
 
-from . import workloads
+from . import _native, workloads
+from . import kernel as kernel_mod
 from .fp8 import dequantize_kv_fp8, quantize_kv_fp8
-from .kernel import DecodeLaunch, _num_sms, balanced_pieces
+from .kernel import DecodeLaunch, _num_sms, balanced_pieces, mla_decode
 from .reference import mla_decode_torch
 from .timing import Flusher, time_us
 
-DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16}
+DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
 CSV_FIELDS = ["gpu", "batch", "seqlen", "heads", "num_splits", "config", "bytes", "triton_us", "eager_us", "compile_us"]
 WORKLOADS = {
     "b1_h128_ctx1k": workloads.b1_h128_1k,
@@ -48,9 +51,11 @@ WORKLOADS = {
 }
 
 
-def make_inputs(batch, seqlen, num_heads, page_size, dtype, device, seed=0):
-    """Uniform-length inputs (the reference's make_inputs recipe, seeded)."""
-    inp = workloads.uniform(batch, num_heads, seqlen, dtype=dtype, seed=seed, page=page_size)
+def make_inputs(batch, seqlen, num_heads, page_size, dtype, device, d_latent=512, d_rope=64, seed=0):
+    """Uniform-length inputs (the reference's make_inputs recipe and
+    arguments, bench.py:20-27, seeded)."""
+    inp = workloads.uniform(batch, num_heads, seqlen, dtype=dtype, seed=seed, page=page_size, d_latent=d_latent,
+                            d_rope=d_rope)
     return inp.to(device)
 
 
@@ -61,7 +66,18 @@ def _splits_arg(text):
 def bench_one(inp, args, device, flush, compiled, writer, gpu):
     splits = _splits_arg(args.splits)
     torch_cache = inp.kv_cache
-    if args.kv_fp8 != "none":
+    generic = inp.head_dim_v != 512 or inp.q.shape[-1] != 576 or inp.q.dtype == torch.float32
+    if generic:
+        if args.kv_fp8 != "none":
+            raise SystemExit("--kv-fp8 runs at --head-dim-v 512 --rope-dim 64 only")
+        if splits is None:
+            splits = kernel_mod._generic_splits(inp.batch, inp.heads, inp.kv_cache.shape[1] * inp.block_table.shape[1],
+                                                _num_sms(device),
+                                                max(_native.load().tmla_generic_heads_per_workgroup(
+                                                    inp.head_dim_v, inp.q.shape[-1] - inp.head_dim_v,
+                                                    _native.DTYPE_CODE[inp.q.dtype]), 1))
+        call = _GenericCall(inp, splits)
+    elif args.kv_fp8 != "none":
         # the HIP decode reads the E4M3 cache; the PyTorch baselines decode the
         # same values dequantised to the input dtype
         codes, scale = quantize_kv_fp8(inp.kv_cache, args.kv_fp8)
@@ -75,7 +91,8 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
     out = call.out
 
     def run_torch(fn):
-        return fn(inp.q, torch_cache, inp.seqlens, inp.block_table, softmax_scale=inp.softmax_scale)
+        return fn(inp.q, torch_cache, inp.seqlens, inp.block_table, head_dim_v=inp.head_dim_v,
+                  softmax_scale=inp.softmax_scale)
 
     t_compile = None
     if compiled is not None:
@@ -97,13 +114,15 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
     nbytes = inp.algorithmic_bytes()
     if args.kv_fp8 != "none":  # one byte per cache element (+ the scales)
         tokens = int(inp.seqlens.sum())
-        nbytes -= tokens * 576
+        nbytes -= tokens * inp.kv_cache.shape[-1]
         nbytes += (scale.numel() * 4)
     flops = inp.flops()
     workers = call.workers or call.splits * inp.batch
     # (the heads per workgroup are chosen inside the library from the call's
     # shape, so the label names the partition only)
     config = "hip/" + (f"balanced{workers}" if splits is None else f"splits{splits}")
+    if generic:
+        config += f"/generic-{inp.head_dim_v}+{inp.q.shape[-1] - inp.head_dim_v}"
     if args.kv_fp8 != "none":
         config += f"/fp8-{args.kv_fp8}"
     seqlen = int(inp.seqlens.max())
@@ -122,6 +141,21 @@ def bench_one(inp, args, device, flush, compiled, writer, gpu):
         writer.writerow({"gpu": gpu, "batch": inp.batch, "seqlen": seqlen, "heads": inp.heads,
                          "num_splits": num_splits, "config": config, "bytes": nbytes, "triton_us": t_hip,
                          "eager_us": t_eager, "compile_us": t_compile})
+
+
+class _GenericCall:
+    """A decode at other head dims or fp32 (the generic kernels through the
+    public mla_decode), with DecodeLaunch's run/out/workers/splits."""
+
+    def __init__(self, inp, splits):
+        self.inp, self.splits, self.workers = inp, splits, 0
+        self.out = None
+
+    def run(self):
+        i = self.inp
+        self.out = mla_decode(i.q, i.kv_cache, i.seqlens, i.block_table, head_dim_v=i.head_dim_v,
+                              softmax_scale=i.softmax_scale, num_splits=self.splits)
+        return self.out
 
 
 def capture_layer_step(model, x, cache, seqlens, bt, device):
@@ -227,6 +261,9 @@ def main(argv=None):
     parser.add_argument("--heads", type=int, default=128, help="128 for one GPU, 16 per GPU under TP8")
     parser.add_argument("--page-size", type=int, default=64)
     parser.add_argument("--dtype", choices=DTYPES, default="bf16")
+    parser.add_argument("--head-dim-v", type=int, default=512,
+                        help="latent dims (make_inputs' d_latent); not 512 runs the generic decode")
+    parser.add_argument("--rope-dim", type=int, default=64, help="RoPE dims (make_inputs' d_rope)")
     parser.add_argument("--compile-mode", default="max-autotune-no-cudagraphs")
     parser.add_argument("--no-eager", action="store_true")
     parser.add_argument("--no-compile", action="store_true", help="skip the torch.compile baseline")
@@ -265,7 +302,8 @@ def main(argv=None):
         writer = csv.DictWriter(csv_file, fieldnames=CSV_FIELDS)
         writer.writeheader()
 
-    print(f"# {gpu}  CUs={_num_sms(device)}  heads={args.heads}  page={args.page_size}  {args.dtype}")
+    print(f"# {gpu}  CUs={_num_sms(device)}  heads={args.heads}  page={args.page_size}  {args.dtype}  "
+          f"dims {args.head_dim_v}+{args.rope_dim}")
     cols = ["batch", "seqlen", "splits", "config", "hip us", "TB/s", "TFLOPS"]
     if not args.no_eager:
         cols.append("eager us")
@@ -277,7 +315,8 @@ def main(argv=None):
     if args.workload:
         cases = [lambda name=name: WORKLOADS[name](dtype).to(device) for name in args.workload]
     else:
-        cases = [lambda b=b, s=s: make_inputs(b, s, args.heads, args.page_size, dtype, device)
+        cases = [lambda b=b, s=s: make_inputs(b, s, args.heads, args.page_size, dtype, device, args.head_dim_v,
+                                              args.rope_dim)
                  for b in args.batch for s in args.seqlen]
     for make in cases:
         inp = make()

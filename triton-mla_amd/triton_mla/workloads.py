@@ -34,10 +34,11 @@ class DecodeInputs:
     seqlens: torch.Tensor
     block_table: torch.Tensor
     softmax_scale: float
+    head_dim_v: int = D_LATENT
 
     def to(self, device):
         return DecodeInputs(self.name, self.q.to(device), self.kv_cache.to(device), self.seqlens.to(device),
-                            self.block_table.to(device), self.softmax_scale)
+                            self.block_table.to(device), self.softmax_scale, self.head_dim_v)
 
     @property
     def batch(self):
@@ -52,26 +53,33 @@ class DecodeInputs:
         src/triton_mla/bench.py:80, with the sum of sequence lengths)."""
         elt = self.q.element_size()
         tokens = int(self.seqlens.sum())
-        return (tokens * self.kv_cache.shape[-1] + self.q.numel() + self.batch * self.heads * D_LATENT) * elt
+        return (tokens * self.kv_cache.shape[-1] + self.q.numel() + self.batch * self.heads * self.head_dim_v) * elt
 
     def flops(self) -> int:
-        """2 * H * (576 + 512) per cached token (src/triton_mla/bench.py:81)."""
-        return int(self.seqlens.sum()) * self.heads * 2 * (self.kv_cache.shape[-1] + D_LATENT)
+        """2 * H * (576 + 512) per cached token at the default dims
+        (src/triton_mla/bench.py:81)."""
+        return int(self.seqlens.sum()) * self.heads * 2 * (self.kv_cache.shape[-1] + self.head_dim_v)
 
 
 def _cdiv(a, b):
     return -(-a // b)
 
 
-def uniform(batch, heads, seqlen, dtype=torch.bfloat16, seed=0, page=PAGE, name=None) -> DecodeInputs:
+def uniform(batch, heads, seqlen, dtype=torch.bfloat16, seed=0, page=PAGE, name=None, d_latent=D_LATENT,
+            d_rope=D_ROPE) -> DecodeInputs:
+    """Uniform lengths; d_latent / d_rope as the reference's make_inputs takes
+    them (bench.py:20). The softmax scale is DeepSeek's 192^-0.5 at the
+    default dims, the mla_decode default (d_latent + d_rope)^-0.5 otherwise."""
     g = torch.Generator().manual_seed(seed)
     pages_per_seq = _cdiv(seqlen, page)
     num_pages = batch * pages_per_seq
-    q = torch.randn(batch, heads, D_LATENT + D_ROPE, generator=g).to(dtype)
-    kv = torch.randn(num_pages, page, D_LATENT + D_ROPE, generator=g).to(dtype)
+    d = d_latent + d_rope
+    q = torch.randn(batch, heads, d, generator=g).to(dtype)
+    kv = torch.randn(num_pages, page, d, generator=g).to(dtype)
     bt = torch.randperm(num_pages, generator=g).view(batch, pages_per_seq).to(torch.int32)
     seqlens = torch.full((batch,), seqlen, dtype=torch.int32)
-    return DecodeInputs(name or f"uniform_b{batch}_h{heads}_s{seqlen}", q, kv, seqlens, bt, 192 ** -0.5)
+    scale = 192 ** -0.5 if (d_latent, d_rope) == (D_LATENT, D_ROPE) else d ** -0.5
+    return DecodeInputs(name or f"uniform_b{batch}_h{heads}_s{seqlen}", q, kv, seqlens, bt, scale, d_latent)
 
 
 def ragged(batch, heads, lo, hi, dtype=torch.bfloat16, seed=0, page=PAGE, name=None) -> DecodeInputs:
