@@ -95,11 +95,12 @@ def test_make_inputs_takes_the_reference_dims():
 
 
 def test_generic_default_splits():
-    """About four 16-head workgroups per compute unit, pieces of >= 256 tokens."""
+    """One vector-ALU workgroup (16 heads) or about four matrix-core
+    workgroups (64 heads) per compute unit, pieces of >= 256 tokens."""
     from triton_mla.kernel import _generic_splits
 
-    assert _generic_splits(32, 128, 8192, 256) == 4  # 256 workgroup groups
-    assert _generic_splits(64, 16, 16384, 256) == 16
+    assert _generic_splits(32, 128, 8192, 256) == 1  # 256 workgroup groups already
+    assert _generic_splits(64, 16, 16384, 256) == 4
     assert _generic_splits(1, 16, 1000, 256) == 4  # capped by the length: cdiv(1000, 256)
     assert _generic_splits(1, 16, 0, 256) == 1
     assert _generic_splits(4096, 128, 1 << 20, 256) == 1

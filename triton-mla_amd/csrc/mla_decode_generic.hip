@@ -199,26 +199,40 @@ __global__ __launch_bounds__(256) void mla_generic_partial_kernel(GenericArgs a)
   const int cpr = D * ES / 16;  // 16-byte chunks per row
   for (int n0 = start; n0 < end; n0 += T) {
     __syncthreads();  // Q staged; the previous step's rows and probabilities read
-    for (int i = tid; i < T * cpr; i += 256) {
-      const int t = i / cpr, ch = i - t * cpr;
-      const int tok = n0 + t;
-      f32x4 v = (f32x4)0.0f;
-      if (tok < end) {
-        const char* src = row_ptr(a, b, tok, ES) + ch * 16;
+    // batches of 8 chunks per thread: their page ids, then their rows, are
+    // in flight together (rows past the piece read its last row, zeroed after)
+    for (int i0 = tid; i0 < T * cpr; i0 += 8 * 256) {
+      const char* src[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int i = min(i0 + 256 * k, T * cpr - 1);
+        const int t = i / cpr, ch = i - t * cpr;
+        src[k] = row_ptr(a, b, min(n0 + t, end - 1), ES) + ch * 16;
+      }
+      f32x4 v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
         if (a.vec) {
-          v = *(const f32x4*)src;
+          v[k] = *(const f32x4*)src[k];
         } else {
-          char* vb = (char*)&v;
+          char* vb = (char*)&v[k];
 #pragma unroll
           for (int e = 0; e < 16; e += ES) {
             if constexpr (ES == 2)
-              *(short*)(vb + e) = *(const short*)(src + e);
+              *(short*)(vb + e) = *(const short*)(src[k] + e);
             else
-              *(float*)(vb + e) = *(const float*)(src + e);
+              *(float*)(vb + e) = *(const float*)(src[k] + e);
           }
         }
       }
-      *(f32x4*)(kvs + t * a.pitch + ch * 16) = v;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int i = i0 + 256 * k;
+        if (i < T * cpr) {
+          const int t = i / cpr, ch = i - t * cpr;
+          *(f32x4*)(kvs + t * a.pitch + ch * 16) = n0 + t < end ? v[k] : (f32x4)0.0f;
+        }
+      }
     }
     __syncthreads();
 

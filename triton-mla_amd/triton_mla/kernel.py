@@ -440,12 +440,15 @@ _GENERIC_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
 def _generic_splits(batch, num_heads, capacity, num_sms, heads_per_wg=16):
-    """Default split count of the generic decode: about four workgroups
-    (heads_per_wg heads, one piece of a sequence) per compute unit, pieces of
-    at least 256 tokens of the cache's capacity, at most 65535 (the launch's
+    """Default split count of the generic decode: about four workgroups per
+    compute unit of the matrix-core form (heads_per_wg 64: short workgroups
+    that hide each other's latency) or one of the vector-ALU form (16: whose
+    per-workgroup set-up costs more than the overlap gains), pieces of at
+    least 256 tokens of the cache's capacity, at most 65535 (the launch's
     grid.y)."""
     groups = max(batch * -(-num_heads // heads_per_wg), 1)
-    by_cus = -(-4 * num_sms // groups)
+    per_cu = 4 if heads_per_wg == 64 else 1
+    by_cus = -(-per_cu * num_sms // groups)
     by_len = max(-(-capacity // 256), 1)
     return max(1, min(by_cus, by_len, 65535))
 
