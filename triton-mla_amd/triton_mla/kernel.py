@@ -559,13 +559,16 @@ _STREAM_WS = {}
 
 
 def _workspace(shape, stream):
+    """(workspace tensor, its address) for a call of `shape` on `stream`."""
     if _capturing():
-        return torch.empty(shape.ws_alloc, dtype=torch.uint8, device=shape.device)
+        ws = torch.empty(shape.ws_alloc, dtype=torch.uint8, device=shape.device)
+        return ws, ws.data_ptr()
     key = (shape.dev_idx, stream)
-    ws = _STREAM_WS.get(key)
-    if ws is None or ws.numel() < shape.ws_alloc:
-        ws = _STREAM_WS[key] = torch.empty(shape.ws_alloc, dtype=torch.uint8, device=shape.device)
-    return ws
+    entry = _STREAM_WS.get(key)  # (tensor, address, bytes)
+    if entry is None or entry[2] < shape.ws_alloc:
+        ws = torch.empty(shape.ws_alloc, dtype=torch.uint8, device=shape.device)
+        entry = _STREAM_WS[key] = (ws, ws.data_ptr(), shape.ws_alloc)
+    return entry[0], entry[1]
 
 
 def _fast_call(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scale, num_splits, want_lse):
@@ -596,15 +599,15 @@ def _fast_call(q, kv_cache, cache_seqlens, block_table, head_dim_v, softmax_scal
     out = q.new_empty(shape.out_shape)
     lse = q.new_empty(shape.lse_shape, dtype=torch.float32) if want_lse else None
     stream = _raw_stream(shape.dev_idx)
-    ws = _workspace(shape, stream)
+    ws, wsp = _workspace(shape, stream)
     btp = None if block_table is None else block_table.data_ptr()
     lsep = None if lse is None else lse.data_ptr()
     if shape.fast is not None:
-        status = shape.fast.decode(shape.plan, qp, kp, btp, cache_seqlens.data_ptr(), out.data_ptr(), lsep,
-                                   ws.data_ptr(), stream)
+        status = shape.fast.decode(shape.plan, qp, kp, btp, cache_seqlens.data_ptr(), out.data_ptr(), lsep, wsp,
+                                   stream)
     else:
         status = shape.fn(qp, *shape.a_q, kp, *shape.a_kv, btp, *shape.a_bt, cache_seqlens.data_ptr(), *shape.a_mid,
-                          out.data_ptr(), *shape.a_out, lsep, ws.data_ptr(), shape.ws_bytes, stream)
+                          out.data_ptr(), *shape.a_out, lsep, wsp, shape.ws_bytes, stream)
     if status:
         _native.check(status, "tmla_mla_decode")
     return out, lse
