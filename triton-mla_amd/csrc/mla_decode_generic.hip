@@ -3,16 +3,17 @@
 // in [16, 256], bf16, fp16 or fp32. It runs the reference's two stages the
 // reference's way (src/triton_mla/kernel.py:43-181): sequence b is cut into
 // num_splits pieces of cdiv(seqlens[b], num_splits) tokens (kernel.py:84-86);
-// a workgroup per (16 heads, piece, sequence) writes a float32 partial and
-// its base-2 log-sum-exp (kernel.py:88-138); a second kernel merges the
-// pieces (kernel.py:141-181).
+// a workgroup per (group of heads, piece, sequence) writes a float32
+// partial and its base-2 log-sum-exp (kernel.py:88-138); a second kernel
+// merges the pieces (kernel.py:141-181).
 //
 // Stage 1 (mla_generic_partial_kernel), 256 threads = 4 waves of 4 heads:
 //   * Q of the 16 heads is staged once in LDS as float, times
 //     softmax_scale * log2(e), so scores are base-2 exponents;
 //   * per step, `tile` cache rows (a power of two <= 64, as many as the LDS
-//     form holds) are copied into LDS with 16-byte loads (element loads when
-//     the cache rows are not 16-byte aligned), rows past the piece zeroed;
+//     form holds) are copied into LDS with 16-byte loads, eight per thread
+//     in flight (element loads when the cache rows are not 16-byte aligned),
+//     rows past the piece zeroed;
 //   * scores: lane l takes token l % tile and every (64 / tile)-th group of 8
 //     dims from group l / tile on, accumulates the partial dot products of
 //     its wave's 4 heads, and the lanes of a token add theirs (xor shuffles);
@@ -386,9 +387,10 @@ __global__ __launch_bounds__(64) void mla_generic_combine_kernel(GenericArgs a) 
 //
 // The same algorithm and partial format on v_mfma_f32_16x16x32: a workgroup
 // of 4 waves takes 64 heads (16 per wave) and steps over 32 tokens:
-//   * the 32 cache rows are loaded into registers one step ahead (16 bytes
-//     per lane and chunk) and written to LDS twice: as rows (the S operand)
-//     and, for the value dims, transposed to [dim][token] (the PV operand);
+//   * the 32 cache rows are loaded into registers one step ahead (units of
+//     4 rows x 16 bytes per lane) and written to LDS twice: as rows (the S
+//     operand) and, for the value dims, transposed to [dim][token] (the PV
+//     operand);
 //   * S (16 heads x 16 tokens, two tiles) = Q . K^T over k-chunks of 32 dims:
 //     lane l reads 8 consecutive dims 32c + 8(l/16) of head l%16 (Q) and of
 //     token l%16 (K), the same k order for both operands; a last chunk of 16
