@@ -95,6 +95,9 @@ def main():
         rt, ck = s[:, :, 0], s[:, :, 1]
         ok = (rt[:, 4] > rt[:, 0]) & (rt[:, 0] > 0)  # workgroups with a segment
         wg = np.nonzero(ok)[0]
+        if wg.size == 0:
+            raise SystemExit(f"workload {args.workload}: no workgroup recorded stamps (the stamps are placed in "
+                             "the 32/64/128-head partial kernels, not in the 16-head or fp8 kernels)")
         rt, ck = rt[ok], ck[ok]
         t0 = rt[:, 0].min()
         if args.spread and it < 6:
