@@ -9,10 +9,12 @@ per phase, the median over workgroups of its duration (microseconds, wall
 clock) and the median over runs: partition (entry to work range), start-up
 (page ids, Q, first copies), loop, finalize (normalisation and stores), the
 shader clock, clocks per 32-token sub-tile, and the parts of one loop
-iteration (first pass: S of the next sub-tile beside half of PV; second
-pass: the rest of PV beside the softmax; then the probabilities' publication
-and the barrier). Stamp slots are defined at phase_stamp in
-csrc/mla_decode.hip.
+iteration (128-head workgroups: the S^T MFMAs of the next sub-tile beside
+the exponentials of this one, then the value MFMAs, then the copy wait and
+the barrier; 32/64-head workgroups: S beside half of PV, the rest of PV
+beside the softmax, the probabilities' publication and the barrier). Stamp
+slots are defined at phase_stamp in csrc/mla_decode.hip; --spread adds the
+per-workgroup percentiles and per-XCD medians of each launch.
 """
 
 from __future__ import annotations
